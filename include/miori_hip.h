@@ -1,0 +1,143 @@
+/*
+ * miori_hip.h -- C ABI of libmiori_hip.so, the MI355X (gfx950) implementation
+ * of Miori's quantized-matmul hot path.
+ *
+ * This ABI replaces, for this path, the reference's Metal device runtime
+ * (src/metal.cpp) and the Metal kernels shaders/ops.metal (gemv4, gemv8,
+ * dequant4, dequant8), shaders/batch.metal (gemv4_b, gemv8_b) and
+ * shaders/gemm_mpp.metal (dequant_tile, gemm_mpp, gemm_mpp32). The C++ shim in
+ * miori_amd/host/ keeps the reference's src/ops.h signatures on top of it.
+ *
+ * Conventions (all entry points):
+ *  - Plain device pointers. The caller owns every buffer. Where the reference
+ *    binds (buffer, byte offset) pairs, the caller passes base + offset.
+ *  - Non-blocking: work is enqueued on `stream` (a hipStream_t; NULL = the
+ *    legacy default stream). miori_sync() waits, like the reference's
+ *    Metal::submit(cb, wait=true) (src/metal.cpp:56-59).
+ *  - Return 0 on success, a negative MIORI_E_* code otherwise; nothing is
+ *    enqueued when a check fails. The reference kernels have no error path
+ *    (unsupported shapes are silently skipped, shaders/batch.metal:156);
+ *    here they are rejected.
+ *  - Thread-safe across distinct streams; calls on one stream are ordered.
+ *
+ * Weight format (MLX affine, src/cpu_ref.h:25-45): W[N][K] quantized in
+ * groups of `group` consecutive elements along K.
+ *  - 4-bit: q uint32 [N][K/8], nibble k of a row at word k/8, bits 4*(k%8).
+ *  - 8-bit: q uint32 [N][K/4], code k at word k/4, bits 8*(k%4).
+ *  - scales, biases: bf16 [N][K/group]; w = float(code)*scale + bias.
+ * Activations are bf16 [M][K] row-major; outputs are [M][N] row-major in
+ * fp32 (out_dtype MIORI_F32, the reference's `device float* y`) or bf16
+ * (MIORI_BF16, round-to-nearest-even as src/cpu_ref.h:16-23).
+ */
+#ifndef MIORI_HIP_H
+#define MIORI_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MIORI_HIP_ABI_VERSION 1
+
+/* status codes */
+#define MIORI_OK 0
+#define MIORI_E_NULL (-1)      /* a required pointer is NULL */
+#define MIORI_E_SHAPE (-2)     /* unsupported M/N/K/group combination */
+#define MIORI_E_ALIGN (-3)     /* pointer misaligned for the kernel's loads */
+#define MIORI_E_DTYPE (-4)     /* unknown out_dtype */
+#define MIORI_E_HIP (-5)       /* a HIP runtime call failed */
+
+/* output element types */
+#define MIORI_F32 0
+#define MIORI_BF16 1
+
+typedef void* miori_stream; /* hipStream_t */
+
+/* Library version (MIORI_HIP_ABI_VERSION). */
+int miori_abi_version(void);
+/* Human-readable text for a status code (static storage). */
+const char* miori_status_string(int status);
+/* Wait for all work enqueued on `stream`
+ * (replaces Metal::submit(cb, wait=true), src/metal.cpp:56-59). */
+int miori_sync(miori_stream stream);
+
+/* ---- decode GEMVs -------------------------------------------------------
+ * 4-bit GEMV, y[1][N] = x[1][K] . dequant4(W)^T, fp32 accumulation.
+ * Replaces gemv4 / gemv4_raw / gemv4x4 / gemv4x2
+ * (src/ops.h:8-10, 113-115, 105-107, 126-128; kernels shaders/ops.metal:6-42,
+ * :563-602, :711-751).
+ * Requires K % 32 == 0, group in {32, 64, 128}, K % group == 0,
+ * K <= 32768, q and x 16-byte aligned. */
+int miori_gemv_q4(const void* q, const void* scales, const void* biases,
+                  const void* x, void* y, uint32_t N, uint32_t K, uint32_t group,
+                  int out_dtype, miori_stream stream);
+
+/* 8-bit GEMV (tied embedding / lm_head). Replaces gemv8 / gemv8_off
+ * (src/ops.h:12-14, 135-138; kernel shaders/ops.metal:46-82).
+ * Requires K % 16 == 0, group in {16, 32, 64, 128}, K % group == 0,
+ * K <= 16384, q and x 16-byte aligned. */
+int miori_gemv_q8(const void* q, const void* scales, const void* biases,
+                  const void* x, void* y, uint32_t N, uint32_t K, uint32_t group,
+                  int out_dtype, miori_stream stream);
+
+/* Batched 4-bit GEMV over M activation rows, y[M][N] = x[M][K] . W^T, with
+ * one pass over the weights for all rows. Replaces gemv4_b
+ * (src/ops.h:164-166; kernel shaders/batch.metal:145-188), which is limited
+ * to M <= 4; here 1 <= M <= 32 (larger M belongs to the GEMMs below).
+ * Same K/group/alignment rules as miori_gemv_q4. */
+int miori_gemv_q4_batched(const void* q, const void* scales, const void* biases,
+                          const void* x, void* y, uint32_t M, uint32_t N,
+                          uint32_t K, uint32_t group, int out_dtype,
+                          miori_stream stream);
+
+/* Batched 8-bit GEMV (batched lm_head). Replaces gemv8_b / gemv8_b_off
+ * (src/ops.h:168-179; kernel shaders/batch.metal:192-236). 1 <= M <= 32.
+ * Same K/group/alignment rules as miori_gemv_q8. */
+int miori_gemv_q8_batched(const void* q, const void* scales, const void* biases,
+                          const void* x, void* y, uint32_t M, uint32_t N,
+                          uint32_t K, uint32_t group, int out_dtype,
+                          miori_stream stream);
+
+/* ---- prefill GEMMs ------------------------------------------------------
+ * C[M][N] = A[M][K] . B[N][K]^T, bf16 operands, fp32 accumulation on MFMA.
+ * B is the bf16 weight cache in this library's layout, which is plain
+ * row-major [N][K] (K contiguous, the operand order MFMA wants); it is what
+ * miori_dequant_q4_tile writes. Replaces gemm_mpp / gemm_mpp_off / gemm_mpp32
+ * (src/ops.h:94-103, 207-209; kernels shaders/gemm_mpp.metal:36-73), whose B
+ * is the Apple-MPP tile-major [N/64][K][64] layout.
+ * Requires K % 64 == 0, N % 16 == 0, A and B 16-byte aligned. */
+int miori_gemm_bf16(const void* A, const void* B, void* C, uint32_t M,
+                    uint32_t N, uint32_t K, int out_dtype, miori_stream stream);
+
+/* Fused 4-bit GEMM: as miori_gemm_bf16 with B = bf16(dequant4(W)), the
+ * dequantisation done while the weight tile is staged to LDS, so the bf16
+ * cache is never materialised. Numerically identical in operands to
+ * miori_dequant_q4_tile followed by miori_gemm_bf16 (the reference's two-step
+ * dequant_tile + gemm_mpp, src/engine.cpp:144-146, 508-518).
+ * Requires K % 64 == 0, N % 16 == 0, group in {32, 64, 128}. */
+int miori_gemm_q4(const void* A, const void* q, const void* scales,
+                  const void* biases, void* C, uint32_t M, uint32_t N, uint32_t K,
+                  uint32_t group, int out_dtype, miori_stream stream);
+
+/* ---- weight-cache builders ----------------------------------------------
+ * out = bf16(float(code)*scale + bias), RNE, bit-exact with the CPU dequant.
+ * dequant_q4_tile writes the layout miori_gemm_bf16 reads (row-major [N][K]);
+ * it replaces dequant_tile (src/ops.h:90-92, shaders/gemm_mpp.metal:9-34).
+ * dequant_q4 replaces dequant4 (src/ops.h:26-28, shaders/ops.metal:142-166),
+ * dequant_q8 replaces dequant8 (src/ops.h:203-205, shaders/ops.metal:754-779);
+ * both write row-major [N][K]. */
+int miori_dequant_q4_tile(const void* q, const void* scales, const void* biases,
+                          void* out, uint32_t N, uint32_t K, uint32_t group,
+                          miori_stream stream);
+int miori_dequant_q4(const void* q, const void* scales, const void* biases,
+                     void* out, uint32_t N, uint32_t K, uint32_t group,
+                     miori_stream stream);
+int miori_dequant_q8(const void* q, const void* scales, const void* biases,
+                     void* out, uint32_t N, uint32_t K, uint32_t group,
+                     miori_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MIORI_HIP_H */

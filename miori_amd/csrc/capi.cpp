@@ -1,0 +1,151 @@
+// C ABI of libmiori_hip.so (declared in include/miori_hip.h): argument
+// checking, then the internal launchers. Nothing is enqueued when a check
+// fails. The reference kernels (shaders/*.metal) have no error path and skip
+// unsupported shapes silently; this layer reports them instead, and the C++
+// shim above it turns a non-zero status into std::runtime_error, the error
+// convention of the reference's Metal::pso (src/metal.cpp:31-37).
+#include "../../include/miori_hip.h"
+#include "kernels.hpp"
+
+#include <hip/hip_runtime.h>
+
+using namespace miori;
+
+namespace {
+
+inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+inline int hip_status(hipError_t e) { return e == hipSuccess ? MIORI_OK : MIORI_E_HIP; }
+
+int check_gemv(int bits, const void* q, const void* s, const void* b, const void* x,
+               const void* y, uint32_t M, uint32_t N, uint32_t K, uint32_t G, int out_dtype) {
+    if (!q || !s || !b || !x || !y) return MIORI_E_NULL;
+    if (out_dtype != MIORI_F32 && out_dtype != MIORI_BF16) return MIORI_E_DTYPE;
+    const uint32_t E = bits == 4 ? 32u : 16u;         // elements per 16-byte chunk
+    const uint32_t kmax = bits == 4 ? 32768u : 16384u; // 4 waves x 64 lanes x 4 chunks
+    if (M == 0 || N == 0 || K == 0 || K % E != 0 || K > kmax) return MIORI_E_SHAPE;
+    if (!(G == 16 || G == 32 || G == 64 || G == 128) || G < E || K % G != 0) return MIORI_E_SHAPE;
+    if (!aligned(q, 16) || !aligned(x, 16) || !aligned(s, 2) || !aligned(b, 2) ||
+        !aligned(y, out_dtype == MIORI_F32 ? 4 : 2))
+        return MIORI_E_ALIGN;
+    return MIORI_OK;
+}
+
+int check_gemm(const void* A, const void* C, uint32_t M, uint32_t N, uint32_t K,
+               int out_dtype) {
+    if (!A || !C) return MIORI_E_NULL;
+    if (out_dtype != MIORI_F32 && out_dtype != MIORI_BF16) return MIORI_E_DTYPE;
+    if (M == 0 || N == 0 || K == 0 || K % 64 != 0 || N % 16 != 0) return MIORI_E_SHAPE;
+    if (!aligned(A, 16) || !aligned(C, out_dtype == MIORI_F32 ? 4 : 2)) return MIORI_E_ALIGN;
+    return MIORI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int miori_abi_version(void) { return MIORI_HIP_ABI_VERSION; }
+
+const char* miori_status_string(int status) {
+    switch (status) {
+        case MIORI_OK: return "ok";
+        case MIORI_E_NULL: return "null pointer argument";
+        case MIORI_E_SHAPE: return "unsupported shape (M/N/K/group)";
+        case MIORI_E_ALIGN: return "misaligned pointer";
+        case MIORI_E_DTYPE: return "unknown output dtype";
+        case MIORI_E_HIP: return "HIP runtime error";
+    }
+    return "unknown status";
+}
+
+int miori_sync(miori_stream stream) {
+    return hip_status(hipStreamSynchronize((hipStream_t)stream));
+}
+
+int miori_gemv_q4(const void* q, const void* scales, const void* biases, const void* x,
+                  void* y, uint32_t N, uint32_t K, uint32_t group, int out_dtype,
+                  miori_stream stream) {
+    int st = check_gemv(4, q, scales, biases, x, y, 1, N, K, group, out_dtype);
+    if (st) return st;
+    return hip_status(launch_gemv_valu(4, q, scales, biases, x, y, 1, N, K, group,
+                                       out_dtype == MIORI_BF16, (hipStream_t)stream));
+}
+
+int miori_gemv_q8(const void* q, const void* scales, const void* biases, const void* x,
+                  void* y, uint32_t N, uint32_t K, uint32_t group, int out_dtype,
+                  miori_stream stream) {
+    int st = check_gemv(8, q, scales, biases, x, y, 1, N, K, group, out_dtype);
+    if (st) return st;
+    return hip_status(launch_gemv_valu(8, q, scales, biases, x, y, 1, N, K, group,
+                                       out_dtype == MIORI_BF16, (hipStream_t)stream));
+}
+
+int miori_gemv_q4_batched(const void* q, const void* scales, const void* biases,
+                          const void* x, void* y, uint32_t M, uint32_t N, uint32_t K,
+                          uint32_t group, int out_dtype, miori_stream stream) {
+    int st = check_gemv(4, q, scales, biases, x, y, M, N, K, group, out_dtype);
+    if (st) return st;
+    if (M > 32) return MIORI_E_SHAPE;
+    return hip_status(launch_gemv_valu(4, q, scales, biases, x, y, M, N, K, group,
+                                       out_dtype == MIORI_BF16, (hipStream_t)stream));
+}
+
+int miori_gemv_q8_batched(const void* q, const void* scales, const void* biases,
+                          const void* x, void* y, uint32_t M, uint32_t N, uint32_t K,
+                          uint32_t group, int out_dtype, miori_stream stream) {
+    int st = check_gemv(8, q, scales, biases, x, y, M, N, K, group, out_dtype);
+    if (st) return st;
+    if (M > 32) return MIORI_E_SHAPE;
+    return hip_status(launch_gemv_valu(8, q, scales, biases, x, y, M, N, K, group,
+                                       out_dtype == MIORI_BF16, (hipStream_t)stream));
+}
+
+int miori_gemm_bf16(const void* A, const void* B, void* C, uint32_t M, uint32_t N,
+                    uint32_t K, int out_dtype, miori_stream stream) {
+    int st = check_gemm(A, C, M, N, K, out_dtype);
+    if (st) return st;
+    if (!B) return MIORI_E_NULL;
+    if (!aligned(B, 16)) return MIORI_E_ALIGN;
+    return hip_status(launch_gemm(A, B, nullptr, nullptr, nullptr, C, M, N, K, 0,
+                                  out_dtype == MIORI_BF16, (hipStream_t)stream));
+}
+
+int miori_gemm_q4(const void* A, const void* q, const void* scales, const void* biases,
+                  void* C, uint32_t M, uint32_t N, uint32_t K, uint32_t group,
+                  int out_dtype, miori_stream stream) {
+    int st = check_gemm(A, C, M, N, K, out_dtype);
+    if (st) return st;
+    if (!q || !scales || !biases) return MIORI_E_NULL;
+    if (!(group == 32 || group == 64 || group == 128) || K % group != 0) return MIORI_E_SHAPE;
+    if (!aligned(q, 16) || !aligned(scales, 2) || !aligned(biases, 2)) return MIORI_E_ALIGN;
+    return hip_status(launch_gemm(A, nullptr, q, scales, biases, C, M, N, K, group,
+                                  out_dtype == MIORI_BF16, (hipStream_t)stream));
+}
+
+static int dequant_common(int bits, const void* q, const void* s, const void* b, void* out,
+                          uint32_t N, uint32_t K, uint32_t G, hipStream_t st) {
+    if (!q || !s || !b || !out) return MIORI_E_NULL;
+    const uint32_t E = bits == 4 ? 32u : 16u;
+    if (N == 0 || K == 0 || K % E != 0) return MIORI_E_SHAPE;
+    if (!(G == 16 || G == 32 || G == 64 || G == 128) || G < E || K % G != 0) return MIORI_E_SHAPE;
+    if (!aligned(q, 16) || !aligned(out, 16) || !aligned(s, 2) || !aligned(b, 2))
+        return MIORI_E_ALIGN;
+    return hip_status(launch_dequant(bits, q, s, b, out, N, K, G, st));
+}
+
+int miori_dequant_q4_tile(const void* q, const void* scales, const void* biases, void* out,
+                          uint32_t N, uint32_t K, uint32_t group, miori_stream stream) {
+    return dequant_common(4, q, scales, biases, out, N, K, group, (hipStream_t)stream);
+}
+
+int miori_dequant_q4(const void* q, const void* scales, const void* biases, void* out,
+                     uint32_t N, uint32_t K, uint32_t group, miori_stream stream) {
+    return dequant_common(4, q, scales, biases, out, N, K, group, (hipStream_t)stream);
+}
+
+int miori_dequant_q8(const void* q, const void* scales, const void* biases, void* out,
+                     uint32_t N, uint32_t K, uint32_t group, miori_stream stream) {
+    return dequant_common(8, q, scales, biases, out, N, K, group, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,31 @@
+// Internal launchers behind the C ABI (no argument checking here; capi.cpp
+// validates shapes, pointers and alignment before calling them).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace miori {
+
+// y[M][N] = x[M][K] . dequant(W)^T on the VALU path (any M; M is split into
+// launches of at most 4 activation rows).
+hipError_t launch_gemv_valu(int bits, const void* q, const void* s, const void* b,
+                            const void* x, void* y, uint32_t M, uint32_t N, uint32_t K,
+                            uint32_t G, int out_bf16, hipStream_t st);
+void gemv_split(int bits, uint32_t K, uint32_t* S, int* cpl);
+
+// Batched GEMV on MFMA (exact affine dequant, per-group fp32 scaling), M <= 32.
+hipError_t launch_gemv_mfma(int bits, const void* q, const void* s, const void* b,
+                            const void* x, void* y, uint32_t M, uint32_t N, uint32_t K,
+                            uint32_t G, int out_bf16, hipStream_t st);
+
+// bf16 -> row-major bf16 dequant.
+hipError_t launch_dequant(int bits, const void* q, const void* s, const void* b, void* out,
+                          uint32_t N, uint32_t K, uint32_t G, hipStream_t st);
+
+// C = A . B^T on MFMA, B bf16 row-major [N][K] (q == nullptr) or 4-bit
+// (q/s/b given, B = bf16(dequant4)).
+hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* s,
+                       const void* b, void* C, uint32_t M, uint32_t N, uint32_t K,
+                       uint32_t G, int out_bf16, hipStream_t st);
+
+}  // namespace miori

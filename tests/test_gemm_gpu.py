@@ -1,0 +1,116 @@
+"""GPU parity of the prefill GEMMs and of the weight-cache dequant builders.
+
+Reference behaviour: shaders/gemm_mpp.metal (dequant_tile + gemm_mpp) and
+shaders/ops.metal:142-166, :754-779 (dequant4 / dequant8). The reference has
+no CPU check of its MPP GEMM (only a 32- vs 64-row self-consistency test,
+src/main.cpp:1403-1443); these tests check against the fp64 oracle
+(src/main.cpp:594-601 loop) under the benchmark tolerance.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from miori_amd import ops, synth
+from tests._check import check_close
+from tests.gpu_util import say, strided_rows
+
+pytestmark = pytest.mark.gpu
+NT = min(16, os.cpu_count() or 1)
+
+
+@pytest.mark.parametrize("bits,N,K,G", [
+    (4, 8192, 2048, 64), (4, 2048, 8192, 64), (4, 48, 256, 32), (4, 16, 512, 128),
+    (8, 1000, 2048, 64), (8, 40, 512, 32), (8, 8, 256, 16),
+])
+def test_dequant_bit_exact(dev, bits, N, K, G):
+    say(f"dequant{bits} N={N} K={K} G={G}")
+    w = synth.quant_weights(N, K, G, bits, seed=N * bits + G)
+    lin = ops.QuantLinear(w, dev)
+    out = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
+    if bits == 4:
+        ops.dequant4(lin.q, lin.s, lin.b, out, N, K, group=G)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(ops.bits_of(out), oracle.dequant_bf16(w.q, w.s, w.b, 4, K, G))
+        out2 = torch.empty_like(out)
+        ops.dequant_tile(lin.q, lin.s, lin.b, out2, N, K, group=G)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(ops.bits_of(out2), ops.bits_of(out))
+    else:
+        ops.dequant8(lin.q, lin.s, lin.b, out, N, K, group=G)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(ops.bits_of(out), oracle.dequant_bf16(w.q, w.s, w.b, 8, K, G))
+
+
+def _operands(M, N, K, seed, dev, G=64):
+    w = synth.quant_weights(N, K, G, 4, seed=seed)
+    Bbits = oracle.dequant_bf16(w.q, w.s, w.b, 4, K, G)
+    A = synth.activations(M, K, seed=seed + 1)
+    return w, Bbits, A
+
+
+def _rows_for(M):
+    if M <= 300:
+        return np.arange(M, dtype=np.int64)
+    return strided_rows(M, 37)
+
+
+@pytest.mark.parametrize("M,K,N", [
+    (256, 2048, 8192), (1024, 2048, 8192), (1472, 2048, 8192),
+    (256, 8192, 2048), (1024, 8192, 2048), (1472, 8192, 2048),
+    (256, 2048, 2560), (1024, 2048, 2560), (1472, 2048, 2560),
+    (1, 64, 16), (23, 128, 80), (300, 192, 144), (64, 2048, 6144),
+])
+def test_gemm_bf16_parity(dev, M, K, N):
+    say(f"gemm_bf16 M={M} K={K} N={N}")
+    w, Bbits, A = _operands(M, N, K, seed=M + N + K, dev=dev)
+    Ad = ops.to_device_bits(A, dev)
+    Bd = ops.to_device_bits(Bbits, dev)
+    C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    ops.gemm_mpp(Ad, Bd, C, M, N, K)
+    torch.cuda.synchronize()
+    rows = _rows_for(M)
+    ref = oracle.gemm_bf16_f64(A, Bbits, rows, nthreads=NT)
+    check_close(ops.bits_of(C)[rows], ref, f"gemm {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("M,K,N,G", [
+    (1024, 2048, 8192, 64), (1472, 8192, 2048, 64), (256, 2048, 2560, 64),
+    (32, 2048, 2048, 64), (32, 8192, 2048, 64), (100, 256, 48, 32), (64, 512, 128, 128),
+])
+def test_gemm_q4_fused_parity(dev, M, K, N, G):
+    """Fused dequant-in-LDS GEMM: against the oracle, and bit-identical to the
+    two-step dequant_tile + gemm_mpp on the same operands."""
+    say(f"gemm_q4 M={M} K={K} N={N} G={G}")
+    w, Bbits, A = _operands(M, N, K, seed=M * 3 + N, dev=dev, G=G)
+    lin = ops.QuantLinear(w, dev)
+    Ad = ops.to_device_bits(A, dev)
+    C = torch.empty((M, N), dtype=torch.float32, device=dev)
+    ops.gemm_q4(Ad, lin.q, lin.s, lin.b, C, M, N, K, group=G)
+    Bd = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
+    ops.dequant_tile(lin.q, lin.s, lin.b, Bd, N, K, group=G)
+    C2 = torch.empty_like(C)
+    ops.gemm_mpp(Ad, Bd, C2, M, N, K)
+    torch.cuda.synchronize()
+    rows = _rows_for(M)
+    ref = oracle.gemm_bf16_f64(A, Bbits, rows, nthreads=NT)
+    check_close(ops.bits_of(C)[rows], ref, f"gemm_q4 {M}x{K}x{N}", f32_tight=True)
+    np.testing.assert_array_equal(ops.bits_of(C), ops.bits_of(C2))
+
+
+def test_gemm_tile_shape_consistency(dev):
+    """The reference's test-mpp-tile property (src/main.cpp:1403-1443): rows
+    0..22 of a 23-row product equal the same rows of the 64-row product."""
+    K, N = 2048, 6144
+    say("gemm 23 vs 64 rows")
+    w, Bbits, A = _operands(64, N, K, seed=4, dev=dev)
+    Ad = ops.to_device_bits(A, dev)
+    Bd = ops.to_device_bits(Bbits, dev)
+    C23 = torch.empty((23, N), dtype=torch.float32, device=dev)
+    C64 = torch.empty((64, N), dtype=torch.float32, device=dev)
+    ops.gemm_mpp32(Ad, Bd, C23, 23, N, K)
+    ops.gemm_mpp(Ad, Bd, C64, 64, N, K)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(C23.cpu().numpy(), C64[:23].cpu().numpy())
