@@ -13,6 +13,8 @@ using namespace miori;
 
 namespace {
 
+constexpr uint64_t kMaxBytes = 0xFFFFFFF0ull;
+
 inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
 inline int hip_status(hipError_t e) { return e == hipSuccess ? MIORI_OK : MIORI_E_HIP; }
@@ -25,10 +27,24 @@ int check_gemv(int bits, const void* q, const void* s, const void* b, const void
     const uint32_t kmax = bits == 4 ? 32768u : 16384u; // 4 waves x 64 lanes x 4 chunks
     if (M == 0 || N == 0 || K == 0 || K % E != 0 || K > kmax) return MIORI_E_SHAPE;
     if (!(G == 16 || G == 32 || G == 64 || G == 128) || G < E || K % G != 0) return MIORI_E_SHAPE;
+    // Kernels address each operand with 32-bit byte offsets.
+    if ((uint64_t)N * K * bits / 8 > kMaxBytes || (uint64_t)M * K * 2 > kMaxBytes ||
+        (uint64_t)M * N * 4 > kMaxBytes)
+        return MIORI_E_SHAPE;
     if (!aligned(q, 16) || !aligned(x, 16) || !aligned(s, 2) || !aligned(b, 2) ||
         !aligned(y, out_dtype == MIORI_F32 ? 4 : 2))
         return MIORI_E_ALIGN;
     return MIORI_OK;
+}
+
+// Batched GEMV: the VALU kernel up to 4 rows (bit-identical to the single-row
+// product, as the reference's gemv4_b is), the MFMA kernel beyond.
+hipError_t launch_batched(int bits, const void* q, const void* s, const void* b,
+                          const void* x, void* y, uint32_t M, uint32_t N, uint32_t K,
+                          uint32_t G, int out_bf16, hipStream_t st) {
+    if (M > 4 && gemv_mfma_supported(bits, M, K, G))
+        return launch_gemv_mfma(bits, q, s, b, x, y, M, N, K, G, out_bf16, st);
+    return launch_gemv_valu(bits, q, s, b, x, y, M, N, K, G, out_bf16, st);
 }
 
 int check_gemm(const void* A, const void* C, uint32_t M, uint32_t N, uint32_t K,
@@ -86,7 +102,7 @@ int miori_gemv_q4_batched(const void* q, const void* scales, const void* biases,
     int st = check_gemv(4, q, scales, biases, x, y, M, N, K, group, out_dtype);
     if (st) return st;
     if (M > 32) return MIORI_E_SHAPE;
-    return hip_status(launch_gemv_valu(4, q, scales, biases, x, y, M, N, K, group,
+    return hip_status(launch_batched(4, q, scales, biases, x, y, M, N, K, group,
                                        out_dtype == MIORI_BF16, (hipStream_t)stream));
 }
 
@@ -96,7 +112,7 @@ int miori_gemv_q8_batched(const void* q, const void* scales, const void* biases,
     int st = check_gemv(8, q, scales, biases, x, y, M, N, K, group, out_dtype);
     if (st) return st;
     if (M > 32) return MIORI_E_SHAPE;
-    return hip_status(launch_gemv_valu(8, q, scales, biases, x, y, M, N, K, group,
+    return hip_status(launch_batched(8, q, scales, biases, x, y, M, N, K, group,
                                        out_dtype == MIORI_BF16, (hipStream_t)stream));
 }
 

@@ -64,6 +64,99 @@ __device__ __forceinline__ uint4 load_stream(const uint4* p) {
     return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+// Buffer resource over [base, base + bytes) (bytes < 4 GiB). Loads whose
+// offset is outside the range return zero, which the kernels use for ragged
+// edges instead of clamping addresses.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+constexpr uint32_t kOOB = 0xFFFFFFF0u;  // an offset that is always out of range
+
+__device__ __forceinline__ u32x4_t buf_load16(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_load_u16(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+
+// (a & m) | c in one v_and_or_b32 (m in an SGPR, c in a VGPR: the VOP3
+// encoding takes no literal and one scalar operand on this target).
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(c));
+    return r;
+}
+
+// Reduce RV (1, 2, 4 or 8) per-lane values over the 64 lanes of a wave.
+// Halves are folded with v_permlane32_swap / v_permlane16_swap (each swap
+// moves one value's partial sums next to another's, so RV values cost about
+// as much as one), then DPP finishes each 16-lane row. On return, value t
+// is complete in every lane of one 16-lane row of one out[] register, as
+// reduce_value() maps it; for RV = 2 value t is in rows 2t and 2t+1; for
+// RV = 1 in all lanes.
+__device__ __forceinline__ void swap32(float& a, float& b) {
+    auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    a = __uint_as_float(p[0]);
+    b = __uint_as_float(p[1]);
+}
+__device__ __forceinline__ void swap16(float& a, float& b) {
+    auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    a = __uint_as_float(p[0]);
+    b = __uint_as_float(p[1]);
+}
+__device__ __forceinline__ float row_sum16(float v) {
+    v += dpp_f32<0xB1>(v);
+    v += dpp_f32<0x4E>(v);
+    v += dpp_f32<0x141>(v);
+    v += dpp_f32<0x140>(v);
+    return v;
+}
+template <int RV>
+__device__ __forceinline__ void wave_reduce(float (&v)[RV], float (&out)[(RV + 3) / 4]) {
+    if constexpr (RV == 1) {
+        float a = v[0], b = v[0];
+        swap32(a, b);
+        float c = a + b, d = c;
+        swap16(c, d);
+        out[0] = row_sum16(c + d);
+    } else if constexpr (RV == 2) {
+        float a = v[0], b = v[1];
+        swap32(a, b);           // lanes 0-31: value 0, lanes 32-63: value 1
+        float c = a + b, d = c;
+        swap16(c, d);
+        out[0] = row_sum16(c + d);
+    } else {
+        constexpr int H = RV / 2;
+        float h[H];
+#pragma unroll
+        for (int i = 0; i < H; ++i) {
+            // pair value i (kept in lanes 0-31) with value i + H (lanes 32-63)
+            float a = v[i], b = v[i + H];
+            swap32(a, b);
+            h[i] = a + b;
+        }
+        // h[i]: lanes 0-31 value i, lanes 32-63 value i + H
+#pragma unroll
+        for (int i = 0; i < H / 2; ++i) {
+            float a = h[2 * i], b = h[2 * i + 1];
+            swap16(a, b);
+            // rows: 0 -> value 2i, 1 -> value 2i+1, 2 -> value 2i+H, 3 -> value 2i+1+H
+            out[i] = row_sum16(a + b);
+        }
+    }
+}
+// Which value register out[i], 16-lane row `row`, holds after wave_reduce:
+// for RV >= 4, rows 0..3 of out[i] hold values 2i, 2i+1, 2i+H, 2i+1+H
+// (H = RV / 2).
+__device__ __forceinline__ int reduce_value(int RV, int i, int row) {
+    if (RV == 1) return 0;
+    if (RV == 2) return row >> 1;
+    const int H = RV / 2;
+    return 2 * i + (row & 1) + ((row >> 1) ? H : 0);
+}
+
 // Store one output element as fp32 or bf16.
 __device__ __forceinline__ void store_out(void* y, size_t idx, float v, bool bf16) {
     if (bf16)

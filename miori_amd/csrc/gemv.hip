@@ -2,15 +2,14 @@
 // small M (1..4 activation rows per launch), 4-bit and 8-bit MLX-affine W.
 //
 // Replaces shaders/ops.metal:6-42 (gemv4), :46-82 (gemv8) and
-// shaders/batch.metal:145-236 (gemv4_b / gemv8_b). The reference kernels put
-// one 32-lane simdgroup on a row, each lane dequantising a 32-element group
-// into fp32 and multiplying by x re-read from memory. Here:
+// shaders/batch.metal:145-236 (gemv4_b / gemv8_b, rows <= 4). The reference
+// kernels put one 32-lane simdgroup on a row, each lane dequantising a
+// 32-element group into fp32 and multiplying by x re-read from memory. Here:
 //
 //  * A lane owns a 16-byte "chunk" of a weight row (32 nibbles or 16 codes)
 //    and one wave instruction loads 64 consecutive chunks, a contiguous 1 KiB
-//    of the row (global_load_dwordx4). A wave works on R rows at once and
-//    issues all of their loads before any arithmetic, so a launch keeps most
-//    of the matrix in flight.
+//    of the row (buffer_load_dwordx4). A wave works on R rows at once and
+//    issues all of their loads before any arithmetic.
 //  * The activation chunk a lane needs is the same for every row, so it is
 //    loaded once and kept in registers, pre-arranged for the unpacking order.
 //  * The affine dequant is factored out of the inner loop:
@@ -20,120 +19,74 @@
 //  * 4-bit: nibble pairs become bf16 pairs with one AND-OR:
 //        ((w >> 4j) & 0x000F000F) | 0x43004300 = bf16(128+q_j), bf16(128+q_{j+4})
 //    and v_dot2c_f32_bf16 multiplies them with the matching x pair, so
-//    D = sum (128+q) x and the bias becomes (b - 128 s).
+//    D = sum (128+q) x and the bias becomes (b - 128 s). 11 VALU ops per
+//    8 weights.
 //  * 8-bit: v_cvt_f32_ubyte{0..3} and an fp32 FMA per code.
-//  * Lane partial sums are reduced with DPP inside the wave; when K is split
-//    across the 4 waves of a workgroup (K > 2048 for 4-bit) the per-wave sums
-//    are added through LDS in a fixed order.
+//  * The R x M row sums are reduced across the wave with permlane swaps and
+//    DPP (wave_reduce); when K is split across the 4 waves of a workgroup
+//    (K > 2048 for 4-bit) the per-wave sums are added through LDS in a fixed
+//    order. Every row's arithmetic is independent of R and M, so a batched
+//    row is bit-identical to the single-row product.
 #include "common.hpp"
 #include "kernels.hpp"
 
 #include <algorithm>
+#include <stdlib.h>
 
 namespace miori {
 
 namespace {
 
-// Load the activation chunk c of one row and arrange it for the unpacking.
-// 4-bit: chunk = 32 bf16 = 16 dwords. For word w of the weight chunk (nibbles
-// k = 8w..8w+7), pair j (j = 0..3) multiplies nibbles j and j+4, so the x pair
-// register holds (x[8w+j], x[8w+j+4]).
+constexpr uint32_t kNibMask = 0x000F000Fu;
+constexpr uint32_t kBf128 = 0x43004300u;   // bf16 pair (128, 128)
+constexpr uint32_t kBfOnes = 0x3F803F80u;  // bf16 pair (1, 1)
+
+// Activation chunk c of one row, arranged for the unpacking order.
+// 4-bit: chunk = 32 bf16 = 16 dwords. For word w of the weight chunk
+// (nibbles k = 8w..8w+7) pair j (j = 0..3) multiplies nibbles j and j+4, so
+// register 4w+j holds the bf16 pair (x[8w+j], x[8w+j+4]).
 // 8-bit: chunk = 16 bf16 kept as 16 fp32.
 template <int BITS>
-__device__ __forceinline__ void load_x_chunk(const uint16_t* __restrict__ xrow, uint32_t c,
-                                             bool valid, uint32_t xr[16], float& xs) {
+__device__ __forceinline__ void prep_x(const u32x4_t (&d)[BITS == 4 ? 4 : 2], uint32_t (&xr)[16],
+                                       float& xs) {
+    float sum = 0.f;
     if constexpr (BITS == 4) {
-        uint32_t d[16];
-        if (valid) {
-            const uint4* p = reinterpret_cast<const uint4*>(xrow) + (size_t)c * 4;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const u32x4_t v = d[w];
+            xr[4 * w + 0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
+            xr[4 * w + 1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
+            xr[4 * w + 2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
+            xr[4 * w + 3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) sum = dot2_bf16(v[t], kBfOnes, sum);
+        }
+    } else {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const uint4 v = p[t];
-                d[4 * t + 0] = v.x; d[4 * t + 1] = v.y; d[4 * t + 2] = v.z; d[4 * t + 3] = v.w;
-            }
-        } else {
-#pragma unroll
-            for (int t = 0; t < 16; ++t) d[t] = 0u;
-        }
-        float sum = 0.f;
-#pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            sum += bf16_bits_to_f32(d[t] & 0xFFFFu);
-            sum += bf16_bits_to_f32(d[t] >> 16);
-        }
-        xs = sum;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t a = d[4 * w + (j >> 1)];
-                const uint32_t b = d[4 * w + 2 + (j >> 1)];
-                xr[4 * w + j] = (j & 1) ? ((a >> 16) | (b & 0xFFFF0000u))
-                                        : ((a & 0xFFFFu) | (b << 16));
-            }
-        }
-    } else {
-        uint32_t d[8];
-        if (valid) {
-            const uint4* p = reinterpret_cast<const uint4*>(xrow) + (size_t)c * 2;
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const uint4 v = p[t];
-                d[4 * t + 0] = v.x; d[4 * t + 1] = v.y; d[4 * t + 2] = v.z; d[4 * t + 3] = v.w;
-            }
-        } else {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) d[t] = 0u;
-        }
-        float sum = 0.f;
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const float lo = bf16_bits_to_f32(d[t] & 0xFFFFu);
-            const float hi = bf16_bits_to_f32(d[t] >> 16);
-            xr[2 * t] = __float_as_uint(lo);
-            xr[2 * t + 1] = __float_as_uint(hi);
-            sum += lo;
-            sum += hi;
-        }
-        xs = sum;
-    }
-}
-
-// sum over the chunk of code_k * x_k (4-bit: of (128 + code_k) * x_k).
-template <int BITS>
-__device__ __forceinline__ float chunk_dot(const uint4 qv, const uint32_t xr[16]) {
-    const uint32_t wv[4] = {qv.x, qv.y, qv.z, qv.w};
-    float d = 0.f;
-    if constexpr (BITS == 4) {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const uint32_t p = ((wv[w] >> (4 * j)) & 0x000F000Fu) | 0x43004300u;
-                d = dot2_bf16(p, xr[4 * w + j], d);
-            }
-        }
-    } else {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float code = (float)((wv[w] >> (8 * j)) & 0xFFu);
-                d = fmaf(code, __uint_as_float(xr[4 * w + j]), d);
+                const uint32_t u = d[h][t];
+                xr[8 * h + 2 * t] = u << 16;
+                xr[8 * h + 2 * t + 1] = u & 0xFFFF0000u;
+                sum = dot2_bf16(u, kBfOnes, sum);
             }
         }
     }
-    return d;
+    xs = sum;
 }
 
 template <int BITS, int MR, int R, int CPL>
 __global__ __launch_bounds__(256) void gemv_valu_kernel(
-    const uint4* __restrict__ q, const uint16_t* __restrict__ s,
-    const uint16_t* __restrict__ bs, const uint16_t* __restrict__ x,
-    void* __restrict__ y, uint32_t N, uint32_t K, uint32_t G, uint32_t S,
-    int out_bf16) {
+    const void* __restrict__ q, const void* __restrict__ s, const void* __restrict__ bs,
+    const void* __restrict__ x, void* __restrict__ y, uint32_t N, uint32_t K, uint32_t G,
+    uint32_t S, int out_bf16) {
     constexpr uint32_t E = (BITS == 4) ? 32u : 16u;  // elements per 16-byte chunk
-    __shared__ float red[4][R][MR];
+    constexpr int XL = (BITS == 4) ? 4 : 2;          // 16-byte x loads per chunk
+    constexpr int RV0 = R * MR;
+    constexpr int RV = RV0 <= 1 ? 1 : RV0 <= 2 ? 2 : RV0 <= 4 ? 4 : 8;
+    static_assert(RV0 <= 8, "at most 8 row sums per wave");
+    __shared__ float red[4][RV];
 
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t wave = threadIdx.x >> 6;
@@ -144,100 +97,141 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(
     const uint32_t C = K / E;       // chunks per row
     const uint32_t ng = K / G;
 
+    const rsrc_t rq = make_rsrc(q, N * C * 16u);
+    const rsrc_t rs = make_rsrc(s, N * ng * 2u);
+    const rsrc_t rb_ = make_rsrc(bs, N * ng * 2u);
+    const rsrc_t rx = make_rsrc(x, MR * K * 2u);
+
     uint32_t cidx[CPL];
     bool cval[CPL];
 #pragma unroll
     for (int i = 0; i < CPL; ++i) {
         const uint32_t c = (js * CPL + i) * 64u + lane;
         cval[i] = c < C;
-        cidx[i] = cval[i] ? c : 0u;
+        cidx[i] = c;
     }
 
-    // Weight loads for all R rows first: they are the HBM stream.
-    uint4 qv[R][CPL];
+    // Weight loads for all R rows first: they are the HBM stream. Rows past
+    // N and chunks past the row read as zero (out-of-range buffer offsets).
+    u32x4_t qv[R][CPL];
     uint32_t sv[R][CPL], bv[R][CPL];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const uint32_t rr = min(row0 + r, N - 1u);
-        const uint4* qrow = q + (size_t)rr * C;
+        const uint32_t row = row0 + r;
+        const bool rv = row < N;
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
-            qv[r][i] = cval[i] ? load_stream(qrow + cidx[i]) : make_uint4(0u, 0u, 0u, 0u);
+            const bool ok = rv && cval[i];
+            qv[r][i] = buf_load16(rq, ok ? (row * C + cidx[i]) * 16u : kOOB);
             const uint32_t g = cidx[i] * E / G;
-            sv[r][i] = s[(size_t)rr * ng + g];
-            bv[r][i] = bs[(size_t)rr * ng + g];
+            const uint32_t so = ok ? (row * ng + g) * 2u : kOOB;
+            sv[r][i] = buf_load_u16(rs, so);
+            bv[r][i] = buf_load_u16(rb_, so);
         }
     }
 
     uint32_t xr[MR][CPL][16];
     float xs[MR][CPL];
 #pragma unroll
-    for (int m = 0; m < MR; ++m)
+    for (int m = 0; m < MR; ++m) {
 #pragma unroll
-        for (int i = 0; i < CPL; ++i)
-            load_x_chunk<BITS>(x + (size_t)m * K, cidx[i], cval[i], xr[m][i], xs[m][i]);
+        for (int i = 0; i < CPL; ++i) {
+            u32x4_t d[XL];
+#pragma unroll
+            for (int t = 0; t < XL; ++t)
+                d[t] = buf_load16(rx, cval[i] ? (m * K + cidx[i] * E) * 2u + t * 16u : kOOB);
+            prep_x<BITS>(d, xr[m][i], xs[m][i]);
+        }
+    }
 
-    float acc[R][MR];
+    float acc[RV];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int m = 0; m < MR; ++m) acc[r][m] = 0.f;
+    for (int v = 0; v < RV; ++v) acc[v] = 0.f;
 
+    const uint32_t c128 = kBf128;
 #pragma unroll
     for (int r = 0; r < R; ++r) {
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
             const float sc = bf16_bits_to_f32(sv[r][i]);
             const float bi = bf16_bits_to_f32(bv[r][i]);
+            float d[MR];
+#pragma unroll
+            for (int m = 0; m < MR; ++m) d[m] = 0.f;
+            if constexpr (BITS == 4) {
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const uint32_t v = qv[r][i][w];
+                    const uint32_t p0 = and_or(v, kNibMask, c128);
+                    const uint32_t p1 = and_or(v >> 4, kNibMask, c128);
+                    const uint32_t p2 = and_or(v >> 8, kNibMask, c128);
+                    const uint32_t p3 = and_or(v >> 12, kNibMask, c128);
+#pragma unroll
+                    for (int m = 0; m < MR; ++m) {
+                        d[m] = dot2_bf16(p0, xr[m][i][4 * w + 0], d[m]);
+                        d[m] = dot2_bf16(p1, xr[m][i][4 * w + 1], d[m]);
+                        d[m] = dot2_bf16(p2, xr[m][i][4 * w + 2], d[m]);
+                        d[m] = dot2_bf16(p3, xr[m][i][4 * w + 3], d[m]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const uint32_t v = qv[r][i][w];
+                    const float c0 = (float)(v & 0xFFu);
+                    const float c1 = (float)((v >> 8) & 0xFFu);
+                    const float c2 = (float)((v >> 16) & 0xFFu);
+                    const float c3 = (float)(v >> 24);
+#pragma unroll
+                    for (int m = 0; m < MR; ++m) {
+                        d[m] = fmaf(c0, __uint_as_float(xr[m][i][4 * w + 0]), d[m]);
+                        d[m] = fmaf(c1, __uint_as_float(xr[m][i][4 * w + 1]), d[m]);
+                        d[m] = fmaf(c2, __uint_as_float(xr[m][i][4 * w + 2]), d[m]);
+                        d[m] = fmaf(c3, __uint_as_float(xr[m][i][4 * w + 3]), d[m]);
+                    }
+                }
+            }
             // 4-bit sums carry the +128 offset of the bf16 trick: fold it into the bias.
             const float bx = (BITS == 4) ? fmaf(-128.f, sc, bi) : bi;
 #pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                const float d = chunk_dot<BITS>(qv[r][i], xr[m][i]);
-                acc[r][m] = fmaf(sc, d, fmaf(bx, xs[m][i], acc[r][m]));
-            }
+            for (int m = 0; m < MR; ++m)
+                acc[r * MR + m] = fmaf(sc, d[m], fmaf(bx, xs[m][i], acc[r * MR + m]));
         }
     }
 
-    float tot[R][MR];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int m = 0; m < MR; ++m) tot[r][m] = wave_sum(acc[r][m]);
+    float tot[(RV + 3) / 4];
+    wave_reduce<RV>(acc, tot);
 
+    // Lane 0 of each 16-lane row that holds a distinct value stores it.
+    const uint32_t row16 = lane >> 4;
+    const bool lead = (lane & 15u) == 0u &&
+                      (RV >= 4 || (RV == 2 ? (row16 & 1u) == 0u : row16 == 0u));
     const bool bf = out_bf16 != 0;
     if (S == 1) {
-        if (lane == 0) {
+        if (lead) {
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const uint32_t row = row0 + r;
-                if (row < N) {
-#pragma unroll
-                    for (int m = 0; m < MR; ++m) store_out(y, (size_t)m * N + row, tot[r][m], bf);
+            for (int i = 0; i < (RV + 3) / 4; ++i) {
+                const int v = reduce_value(RV, i, (int)row16);
+                if (v < RV0) {
+                    const uint32_t row = row0 + v / MR;
+                    const uint32_t m = v % MR;
+                    if (row < N) store_out(y, (size_t)m * N + row, tot[i], bf);
                 }
             }
         }
         return;
     }
-    if (lane == 0) {
+    if (lead) {
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int m = 0; m < MR; ++m) red[wave][r][m] = tot[r][m];
+        for (int i = 0; i < (RV + 3) / 4; ++i) red[wave][reduce_value(RV, i, (int)row16)] = tot[i];
     }
     __syncthreads();
-    if (js == 0 && lane == 0) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const uint32_t row = row0 + r;
-            if (row >= N) continue;
-#pragma unroll
-            for (int m = 0; m < MR; ++m) {
-                float v = red[wave][r][m];
-                for (uint32_t j = 1; j < S; ++j) v += red[wave + j][r][m];
-                store_out(y, (size_t)m * N + row, v, bf);
-            }
-        }
+    if (js == 0 && lane < (uint32_t)RV0) {
+        const uint32_t v = lane;
+        float t = red[wave][v];
+        for (uint32_t j = 1; j < S; ++j) t += red[wave + j][v];
+        const uint32_t row = row0 + v / MR;
+        if (row < N) store_out(y, (size_t)(v % MR) * N + row, t, bf);
     }
 }
 
@@ -248,8 +242,7 @@ hipError_t launch_valu(const void* q, const void* s, const void* b, const void* 
     const uint32_t rows_per_wg = R * (4u / S);
     const uint32_t grid = (N + rows_per_wg - 1) / rows_per_wg;
     hipLaunchKernelGGL((gemv_valu_kernel<BITS, MR, R, CPL>), dim3(grid), dim3(256), 0, st,
-                       (const uint4*)q, (const uint16_t*)s, (const uint16_t*)b,
-                       (const uint16_t*)x, y, N, K, G, S, out_bf16);
+                       q, s, b, x, y, N, K, G, S, out_bf16);
     return hipGetLastError();
 }
 
@@ -313,7 +306,8 @@ hipError_t launch_gemv_valu(int bits, const void* q, const void* s, const void* 
     uint32_t S;
     int cpl;
     gemv_split(bits, K, &S, &cpl);
-    static const int rows_m1 = env_int("MIORI_GEMV_ROWS", 4);
+    // rows per wave for M = 1 (MIORI_GEMV_ROWS overrides it for tuning sweeps)
+    const int rows_m1 = env_int("MIORI_GEMV_ROWS", 4);
     const int mr_max = cpl == 1 ? 4 : (cpl == 2 ? 2 : 1);
     const size_t ybytes = out_bf16 ? 2 : 4;
     for (uint32_t m0 = 0; m0 < M; m0 += mr_max) {

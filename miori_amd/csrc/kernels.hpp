@@ -13,6 +13,7 @@ hipError_t launch_gemv_valu(int bits, const void* q, const void* s, const void* 
                             uint32_t G, int out_bf16, hipStream_t st);
 void gemv_split(int bits, uint32_t K, uint32_t* S, int* cpl);
 
+bool gemv_mfma_supported(int bits, uint32_t M, uint32_t K, uint32_t G);
 // Batched GEMV on MFMA (exact affine dequant, per-group fp32 scaling), M <= 32.
 hipError_t launch_gemv_mfma(int bits, const void* q, const void* s, const void* b,
                             const void* x, void* y, uint32_t M, uint32_t N, uint32_t K,
