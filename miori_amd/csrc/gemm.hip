@@ -1,45 +1,109 @@
 // Prefill GEMM on bf16 MFMA for gfx950: C[M][N] = A[M][K] . B[N][K]^T with
 // fp32 accumulation, B either the bf16 weight cache (row-major [N][K]) or the
-// 4-bit MLX-affine weights dequantised to bf16 while the tile is staged to LDS.
+// 4-bit MLX-affine weights dequantised to bf16 on the way into LDS.
 //
 // Replaces shaders/gemm_mpp.metal:36-73 (gemm_mpp / gemm_mpp32, Apple MPP
 // matmul2d on a tile-major bf16 cache) and, for the fused variant, the
 // two-step dequant_tile + gemm_mpp of src/engine.cpp:144-146, 508-518.
 //
-// Structure: a 256x128 (M x N) macro tile per 256-thread workgroup, K in
-// steps of 64. The four waves form a 2x2 grid of 128x64 wave tiles, each a
-// 4x2 array of v_mfma_f32_32x32x16_bf16 accumulators. Operand tiles are
-// double-buffered in LDS (A 32 KiB + B 16 KiB per stage); global loads of
-// step k+1 are in flight while step k runs on the matrix cores. Rows in LDS
-// are 128 bytes (64 bf16) and the eight 16-byte chunks of a row are XOR-
-// swizzled by (row & 7), so the 32 rows an MFMA fragment read touches fall in
-// distinct banks. Workgroups are renumbered so that each XCD (workgroup id
-// mod 8 on MI355X) works on a contiguous block of output tiles and shares its
-// operand slabs in its own L2.
+// Structure (BM x BN macro tile per 256-thread workgroup, K in steps of 64):
+//  * Operand tiles move HBM/L2 -> LDS with global_load_lds_dwordx4 (gfx950
+//    direct-to-LDS DMA): no staging registers, and the loads of step k+2 are
+//    in flight while step k runs on the matrix cores (3-stage LDS ring, one
+//    workgroup barrier per step, vmcnt waits placed by hand).
+//  * Rows in LDS are 128 bytes (64 bf16); the 16-byte chunk kb of row r sits
+//    at slot kb ^ (r & 7) ^ ((r >> 3) & 1), so the 32 rows of an MFMA
+//    fragment read hit distinct banks. The DMA writes lanes in order, so the
+//    swizzle is applied by choosing which global chunk each lane fetches.
+//  * Four waves in a 2x2 grid, each a (BM/2) x (BN/2) tile of
+//    v_mfma_f32_32x32x16_bf16 accumulators. In k-step s of a 64-wide K tile,
+//    lane half h = lane/32 of a fragment holds chunk 4h + s (any k order is
+//    valid as long as A and B use the same one).
+//  * Fused 4-bit B: the raw codes (32 bytes per row per K tile) and the
+//    per-group scale/bias are DMA'd like A, one step ahead; every thread then
+//    dequantises one 32-code chunk (bf16_rne(q*s + b), the exact bf16 value
+//    the dequant kernels write) into a double-buffered bf16 B tile. The MFMA
+//    operands are therefore identical to the two-step path, and so are the
+//    results, bit for bit.
+//  * Workgroups are renumbered so each XCD (workgroup id mod 8) works on a
+//    contiguous block of output tiles and keeps its operand slabs in its own
+//    L2. The epilogue packs column pairs across lanes (DPP) for 4-byte bf16
+//    stores.
 #include "common.hpp"
 #include "kernels.hpp"
+
+#include <stdlib.h>
 
 namespace miori {
 
 namespace {
 
-constexpr int BM = 256, BN = 128, BK = 64;
-constexpr int ROWB = BK * 2;                 // bytes per LDS row
-constexpr int A_BYTES = BM * ROWB;           // 32 KiB
-constexpr int B_BYTES = BN * ROWB;           // 16 KiB
-constexpr int STAGE = A_BYTES + B_BYTES;
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef const __attribute__((address_space(1))) void* gptr_t;
 
-__device__ __forceinline__ uint32_t swz(uint32_t row, uint32_t kb) {
-    return row * ROWB + ((kb ^ (row & 7u)) << 4);
+constexpr int BK = 64;
+constexpr int ROWB = BK * 2;  // bytes per LDS row of a bf16 tile
+
+__device__ __forceinline__ uint32_t swz(uint32_t r, uint32_t kb) {
+    return r * ROWB + ((kb ^ (r & 7u) ^ ((r >> 3) & 1u)) << 4);
 }
 
-template <bool Q4>
+__device__ __forceinline__ void dma16(const void* g, uint8_t* l) {
+    __builtin_amdgcn_global_load_lds((gptr_t)g, (lds_ptr_t)l, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* g, uint8_t* l) {
+    __builtin_amdgcn_global_load_lds((gptr_t)g, (lds_ptr_t)l, 4, 0, 0);
+}
+__device__ __forceinline__ void dma2(const void* g, uint8_t* l) {
+    __builtin_amdgcn_global_load_lds((gptr_t)g, (lds_ptr_t)l, 2, 0, 0);
+}
+
+// Workgroup barrier that neither waits for outstanding DMA (the fence of
+// __syncthreads would) nor lets the compiler move memory accesses across it.
+__device__ __forceinline__ void barrier_lds() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int BM, int BN, bool Q4, int G>
+struct Cfg {
+    static constexpr int WM = BM / 2, WN = BN / 2;   // wave tile
+    static constexpr int TM = WM / 32, TN = WN / 32; // 32x32 MFMA tiles per wave
+    static constexpr int A_ST = BM * ROWB;
+    static constexpr int B_ST = BN * ROWB;
+    static constexpr int RAW_ST = BN * 32;          // 4-bit codes: 32 B per row per K tile
+    // scale/bias bytes per row per K tile in LDS: the DMA writes one dword per
+    // lane whatever the load size, so each row gets a 4-byte slot (G = 32: the
+    // two groups of the K tile; otherwise one bf16 in the low half)
+    static constexpr int SB_W = 4;
+    static constexpr int SB_ST = BN * SB_W;
+    static constexpr int A_OFF = 0;
+    static constexpr int B_OFF = 3 * A_ST;          // bf16 B ring (3 stages)
+    static constexpr int RAW_OFF = B_OFF + 3 * B_ST;
+    static constexpr int S_OFF = RAW_OFF + 3 * RAW_ST;
+    static constexpr int BI_OFF = S_OFF + 3 * SB_ST;
+    static constexpr int LDS = Q4 ? BI_OFF + 3 * SB_ST : RAW_OFF;
+    // DMA instructions per wave per K tile (each moves 64 lanes x size bytes)
+    static constexpr int A_INS = BM / 32;
+    static constexpr int B_INS = Q4 ? 0 : BN / 32;
+    static constexpr int RAW_INS = Q4 ? BN * 32 / 1024 / 4 : 0;             // per wave
+    static constexpr int SB_INS = Q4 ? BN / 64 / 2 : 0;   // per wave (s or b), 64 rows each
+    static constexpr int L = A_INS + B_INS + RAW_INS + SB_INS;
+    static_assert(!Q4 || BN == 128, "fused dequant maps one thread per 32-code chunk");
+};
+
+template <int BM, int BN, bool Q4, int G>
 __global__ __launch_bounds__(256) void gemm_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
-    const uint4* __restrict__ q, const uint16_t* __restrict__ s,
+    const uint32_t* __restrict__ q, const uint16_t* __restrict__ s,
     const uint16_t* __restrict__ bsc, void* __restrict__ C, uint32_t M, uint32_t N,
-    uint32_t K, uint32_t G, int out_bf16, uint32_t tiles_m) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * STAGE];
+    uint32_t K, int out_bf16, uint32_t tiles_m, int remap) {
+    using CF = Cfg<BM, BN, Q4, G>;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[CF::LDS];
 
     const uint32_t t = threadIdx.x;
     const uint32_t lane = t & 63u, wave = t >> 6;
@@ -47,126 +111,245 @@ __global__ __launch_bounds__(256) void gemm_kernel(
 
     uint32_t pid = blockIdx.x;
     const uint32_t nwg = gridDim.x;
-    if ((nwg & 7u) == 0) pid = (pid & 7u) * (nwg >> 3) + (pid >> 3);
+    if (remap && (nwg & 7u) == 0) pid = (pid & 7u) * (nwg >> 3) + (pid >> 3);
     const uint32_t tm = pid % tiles_m, tn = pid / tiles_m;
     const uint32_t m0 = tm * BM, n0 = tn * BN;
     const uint32_t KT = K / BK;
+    const uint32_t ng = Q4 ? K / G : 1;
 
-    // ---- global -> register staging
-    uint4 ra[8];
-    uint4 rb[Q4 ? 1 : 4];
-    uint32_t rs = 0, rbias = 0;
-
-    auto load_tiles = [&](uint32_t kt) {
+    // Per-lane DMA source rows (clamped: rows past M / N load valid memory and
+    // their results are never stored).
+    // One DMA group: A(kt) into A stage `stage_a`; bf16 B(kt) into B stage
+    // `stage_b`, or, fused, the raw codes + scale/bias of K tile `kr` into raw
+    // slot `stage_b`. with_a = false issues only the B part.
+    auto issue = [&](uint32_t kt, uint32_t stage_a, uint32_t kr, uint32_t stage_b, bool with_a) {
+        if (with_a) {
+            // A: instruction p of this wave covers 8 rows; lane -> (row, physical chunk)
 #pragma unroll
-        for (int p = 0; p < 8; ++p) {
-            const uint32_t row = min(m0 + p * 32 + (t >> 3), M - 1u);
-            ra[p] = *reinterpret_cast<const uint4*>(A + (size_t)row * K + kt * BK + (t & 7u) * 8);
+            for (int p = 0; p < CF::A_INS; ++p) {
+                const uint32_t r0 = (wave * CF::A_INS + p) * 8u;
+                const uint32_t r = r0 + (lane >> 3);
+                const uint32_t kb = (lane & 7u) ^ (r & 7u) ^ ((r >> 3) & 1u);
+                const uint32_t row = min(m0 + r, M - 1u);
+                dma16(A + (size_t)row * K + kt * BK + kb * 8u,
+                      lds + CF::A_OFF + stage_a * CF::A_ST + r0 * ROWB);
+            }
         }
-        if constexpr (Q4) {
-            const uint32_t row = min(n0 + (t >> 1), N - 1u);
-            const uint32_t half = t & 1u;
-            rb[0] = q[(size_t)row * (K / 32) + kt * 2 + half];
-            const uint32_t g = (kt * BK + half * 32) / G;
-            rs = s[(size_t)row * (K / G) + g];
-            rbias = bsc[(size_t)row * (K / G) + g];
-        } else {
+        if constexpr (!Q4) {
 #pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                const uint32_t row = min(n0 + p * 32 + (t >> 3), N - 1u);
-                rb[p] = *reinterpret_cast<const uint4*>(B + (size_t)row * K + kt * BK + (t & 7u) * 8);
+            for (int p = 0; p < CF::B_INS; ++p) {
+                const uint32_t r0 = (wave * CF::B_INS + p) * 8u;
+                const uint32_t r = r0 + (lane >> 3);
+                const uint32_t kb = (lane & 7u) ^ (r & 7u) ^ ((r >> 3) & 1u);
+                const uint32_t row = min(n0 + r, N - 1u);
+                dma16(B + (size_t)row * K + kt * BK + kb * 8u, lds + CF::B_OFF + stage_b * CF::B_ST + r0 * ROWB);
+            }
+        } else {
+            // raw codes of K tile kt (clamped to a valid tile): row r, chunk c at slot 2r + c
+            const uint32_t ktc = min(kr, KT - 1u);
+            {
+                const uint32_t slot = wave * 64u + lane;
+                const uint32_t r = slot >> 1, c = slot & 1u;
+                const uint32_t row = min(n0 + r, N - 1u);
+                dma16(q + (size_t)row * (K / 8) + ktc * 8u + c * 4u,
+                      lds + CF::RAW_OFF + stage_b * CF::RAW_ST + wave * 1024u);
+            }
+            // scales (waves 0,1) or biases (waves 2,3): 64 rows per instruction
+            {
+                const uint32_t r = (wave & 1u) * 64u + lane;
+                const uint32_t row = min(n0 + r, N - 1u);
+                const uint16_t* src = (wave < 2) ? s : bsc;
+                uint8_t* dst = lds + ((wave < 2) ? CF::S_OFF : CF::BI_OFF) + stage_b * CF::SB_ST +
+                               (wave & 1u) * 64u * CF::SB_W;
+                if constexpr (G == 32)
+                    dma4(src + (size_t)row * ng + ktc * 2u, dst);
+                else
+                    dma2(src + (size_t)row * ng + ktc * BK / G, dst);
             }
         }
     };
 
-    auto store_tiles = [&](int buf) {
-        uint8_t* base = lds + buf * STAGE;
+    // Fused 4-bit: dequantise raw slot `stage` into bf16 buffer bb.
+    auto dequant_tile = [&](uint32_t stage, uint32_t bb) {
+        const uint32_t r = t >> 1, c = t & 1u;
+        const u32x4_t raw = *reinterpret_cast<const u32x4_t*>(lds + CF::RAW_OFF + stage * CF::RAW_ST + t * 16u);
+        const uint8_t* sp = lds + CF::S_OFF + stage * CF::SB_ST + r * CF::SB_W;
+        const uint8_t* bp = lds + CF::BI_OFF + stage * CF::SB_ST + r * CF::SB_W;
+        const uint32_t sub = (G == 32) ? c * 2u : 0u;  // G = 32: the chunk's own group
+        const float sc = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(sp + sub));
+        const float bi = bf16_bits_to_f32(*reinterpret_cast<const uint16_t*>(bp + sub));
+        uint8_t* dst = lds + CF::B_OFF + bb * CF::B_ST;
 #pragma unroll
-        for (int p = 0; p < 8; ++p) {
-            const uint32_t r = p * 32 + (t >> 3);
-            *reinterpret_cast<uint4*>(base + swz(r, t & 7u)) = ra[p];
-        }
-        uint8_t* bb = base + A_BYTES;
-        if constexpr (Q4) {
-            const uint32_t r = t >> 1, half = t & 1u;
-            const float sc = bf16_bits_to_f32(rs), bi = bf16_bits_to_f32(rbias);
-            const uint32_t wv[4] = {rb[0].x, rb[0].y, rb[0].z, rb[0].w};
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t v = raw[w];
+            const uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
+            float f[8];
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                uint32_t o[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float v0 = fmaf((float)((wv[w] >> (8 * j)) & 0xFu), sc, bi);
-                    const float v1 = fmaf((float)((wv[w] >> (8 * j + 4)) & 0xFu), sc, bi);
-                    o[j] = pack_bf16x2(v0, v1);
-                }
-                *reinterpret_cast<uint4*>(bb + swz(r, half * 4 + w)) = make_uint4(o[0], o[1], o[2], o[3]);
+            for (int j = 0; j < 4; ++j) {
+                f[2 * j] = fmaf((float)((lo >> (8 * j)) & 0xFFu), sc, bi);
+                f[2 * j + 1] = fmaf((float)((hi >> (8 * j)) & 0xFFu), sc, bi);
             }
-        } else {
+            u32x4_t o;
 #pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                const uint32_t r = p * 32 + (t >> 3);
-                *reinterpret_cast<uint4*>(bb + swz(r, t & 7u)) = rb[p];
+            for (int j = 0; j < 4; ++j) {
+                bf16x2_t p = {(__bf16)f[2 * j], (__bf16)f[2 * j + 1]};
+                o[j] = __builtin_bit_cast(uint32_t, p);
             }
+            *reinterpret_cast<u32x4_t*>(dst + swz(r, c * 4u + w)) = o;
         }
     };
 
-    f32x16_t acc[4][2];
+    f32x16_t acc[CF::TM][CF::TN];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < CF::TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < CF::TN; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-    load_tiles(0);
-    store_tiles(0);
-    __syncthreads();
+    // MFMA fragments, double-buffered: k-step ks+1 is read while ks runs.
+    // The reads are issued as inline asm with hand-placed lgkmcnt waits (the
+    // compiler's own waits drain every LDS read before each MFMA group). A
+    // fragment row r = (multiple of 16) + lane%32, so its swizzle term is
+    // f = (lane & 7) ^ ((lane >> 3) & 1) for every fragment, and k-step ks of
+    // lane half h reads chunk (4h ^ f) ^ ks.
+    bf16x8_t af[2][CF::TM], bf[2][CF::TN];
+    const uint32_t fsw = (lane & 7u) ^ ((lane >> 3) & 1u);
+    const uint32_t c0 = (4u * (lane >> 5)) ^ fsw;
+    const uint32_t lrow = (lane & 31u) * ROWB;
+    auto read_frags = [&](uint32_t kt, int ks, int slot) {
+        const uint32_t chunk = ((c0 ^ (uint32_t)ks) << 4) + lrow;
+        const uint32_t a_addr = CF::A_OFF + (kt % 3) * CF::A_ST + wm * CF::WM * ROWB + chunk;
+        const uint32_t b_addr = CF::B_OFF + (kt % 3) * CF::B_ST + wn * CF::WN * ROWB + chunk;
+#pragma unroll
+        for (int i = 0; i < CF::TM; ++i)
+            asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(af[slot][i]) : "v"(a_addr), "i"(i * 32 * ROWB));
+#pragma unroll
+        for (int j = 0; j < CF::TN; ++j)
+            asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(bf[slot][j]) : "v"(b_addr), "i"(j * 32 * ROWB));
+    };
+    constexpr int NFR = CF::TM + CF::TN;  // LDS reads per k-step
+    auto mfmas = [&](int slot) {
+#pragma unroll
+        for (int i = 0; i < CF::TM; ++i)
+#pragma unroll
+            for (int j = 0; j < CF::TN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][i], bf[slot][j],
+                                                                    acc[i][j], 0, 0, 0);
+    };
+
+    // Pipeline. Group p = {A(p), B(p)} (bf16) or {A(p), raw(p+1)} (fused; the
+    // codes travel one group early and are dequantised two tiles ahead into a
+    // 3-deep bf16 ring). Groups 0..2 are issued up front; in step kt the
+    // barrier sits before the last k-step, where tile kt's LDS reads are done:
+    // it publishes group kt+1, frees stage kt % 3 for group kt+3, and the
+    // first fragments of tile kt+1 are read while the last MFMAs of kt run.
+    if constexpr (Q4) {
+        issue(0, 0, 0, 0, false);  // raw(0)
+        issue(0, 0, 1, 1, true);
+        if (KT > 1) issue(1, 1, 2, 2, true);
+        if (KT > 1) wait_vm<CF::L>(); else wait_vm<0>();
+        barrier_lds();
+        dequant_tile(0, 0);
+        if (KT > 1) dequant_tile(1, 1);
+        barrier_lds();             // raw slot 0 is free again
+        if (KT > 2) issue(2, 2, 3, 0, true);
+    } else {
+        issue(0, 0, 0, 0, true);
+        if (KT > 1) issue(1, 1, 1, 1, true);
+        if (KT > 2) issue(2, 2, 2, 2, true);
+        if (KT > 2) wait_vm<2 * CF::L>(); else if (KT > 1) wait_vm<CF::L>(); else wait_vm<0>();
+        barrier_lds();
+    }
+    read_frags(0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
 
     for (uint32_t kt = 0; kt < KT; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < KT) load_tiles(kt + 1);
-        const uint8_t* base = lds + buf * STAGE;
 #pragma unroll
-        for (int ks = 0; ks < BK / 16; ++ks) {
-            const uint32_t kb = 2 * ks + (lane >> 5);
-            bf16x8_t af[4], bf[2];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t r = wm * 128 + i * 32 + (lane & 31u);
-                af[i] = *reinterpret_cast<const bf16x8_t*>(base + swz(r, kb));
-            }
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const uint32_t r = wn * 64 + j * 32 + (lane & 31u);
-                bf[j] = *reinterpret_cast<const bf16x8_t*>(base + A_BYTES + swz(r, kb));
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        for (int ks = 0; ks < BK / 16 - 1; ++ks) {
+            read_frags(kt, ks + 1, (ks + 1) & 1);
+            asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(NFR) : "memory");  // k-step ks has landed
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(ks & 1);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        if (kt + 1 < KT) store_tiles(buf ^ 1);
-        __syncthreads();
+        if (kt + 1 < KT) {
+            if (kt + 2 < KT) wait_vm<CF::L>(); else wait_vm<0>();
+            barrier_lds();  // also completes the reads of the last k-step
+            if constexpr (Q4) {
+                if (kt + 2 < KT) dequant_tile((kt + 2) % 3, (kt + 2) % 3);
+                if (kt + 3 < KT) issue(kt + 3, kt % 3, kt + 4, (kt + 4) % 3, true);
+            } else {
+                if (kt + 3 < KT) issue(kt + 3, kt % 3, kt + 3, kt % 3, true);
+            }
+            read_frags(kt + 1, 0, 0);
+        } else {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas((BK / 16 - 1) & 1);
+        __builtin_amdgcn_sched_barrier(0);
     }
 
-    // ---- epilogue: lane l of a 32x32 accumulator holds column l%32 and rows
-    // 8*(e/4) + 4*(l/32) + e%4 for its 16 elements e.
-    const bool bf = out_bf16 != 0;
+    // Epilogue. Accumulator element e of lane l is row 8*(e/4) + 4*(l/32) + e%4,
+    // column l%32 of its 32x32 tile. For bf16 output, lanes 2p and 2p+1 swap
+    // one value each (DPP) so that each holds two adjacent columns of one row.
+    const bool odd = lane & 1u;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < CF::TM; ++i) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint32_t col = n0 + wn * 64 + j * 32 + (lane & 31u);
-            if (col >= N) continue;
+        for (int j = 0; j < CF::TN; ++j) {
+            const uint32_t col = n0 + wn * CF::WN + j * 32 + (lane & 31u);
+            const uint32_t rbase = m0 + wm * CF::WM + i * 32 + 4u * (lane >> 5);
+            if (out_bf16) {
+                const uint32_t ce = col & ~1u;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const uint32_t row = m0 + wm * 128 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                if (row < M) store_out(C, (size_t)row * N + col, acc[i][j][e], bf);
+                for (int e = 0; e < 16; e += 2) {
+                    const float send = odd ? acc[i][j][e] : acc[i][j][e + 1];
+                    const float recv = dpp_f32<0xB1>(send);
+                    const float lo = odd ? recv : acc[i][j][e];
+                    const float hi = odd ? acc[i][j][e + 1] : recv;
+                    const uint32_t row = rbase + 8u * (e >> 2) + (e & 3) + (odd ? 1u : 0u);
+                    bf16x2_t p = {(__bf16)lo, (__bf16)hi};
+                    if (row < M && ce < N)
+                        *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(C) + (size_t)row * N + ce) =
+                            __builtin_bit_cast(uint32_t, p);
+                }
+            } else if (col < N) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const uint32_t row = rbase + 8u * (e >> 2) + (e & 3);
+                    if (row < M) reinterpret_cast<float*>(C)[(size_t)row * N + col] = acc[i][j][e];
+                }
             }
         }
     }
+}
+
+template <int BM, int BN, bool Q4, int G>
+hipError_t launch_cfg(const void* A, const void* B, const void* q, const void* s, const void* b,
+                      void* C, uint32_t M, uint32_t N, uint32_t K, int out_bf16, hipStream_t st) {
+    const uint32_t tiles_m = (M + BM - 1) / BM;
+    const uint32_t tiles_n = (N + BN - 1) / BN;
+    const int remap = getenv("MIORI_GEMM_REMAP") ? atoi(getenv("MIORI_GEMM_REMAP")) : 1;
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, Q4, G>), dim3(tiles_m * tiles_n), dim3(256), 0, st,
+                       (const uint16_t*)A, (const uint16_t*)B, (const uint32_t*)q,
+                       (const uint16_t*)s, (const uint16_t*)b, C, M, N, K, out_bf16, tiles_m,
+                       remap);
+    return hipGetLastError();
+}
+
+template <int BM, int BN>
+hipError_t launch_tile(const void* A, const void* B, const void* q, const void* s, const void* b,
+                       void* C, uint32_t M, uint32_t N, uint32_t K, uint32_t G, int out_bf16,
+                       hipStream_t st) {
+    if (!q) return launch_cfg<BM, BN, false, 64>(A, B, q, s, b, C, M, N, K, out_bf16, st);
+    switch (G) {
+        case 32: return launch_cfg<BM, BN, true, 32>(A, B, q, s, b, C, M, N, K, out_bf16, st);
+        case 64: return launch_cfg<BM, BN, true, 64>(A, B, q, s, b, C, M, N, K, out_bf16, st);
+        case 128: return launch_cfg<BM, BN, true, 128>(A, B, q, s, b, C, M, N, K, out_bf16, st);
+    }
+    return hipErrorInvalidValue;
 }
 
 }  // namespace
@@ -174,18 +357,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(
 hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* s,
                        const void* b, void* C, uint32_t M, uint32_t N, uint32_t K,
                        uint32_t G, int out_bf16, hipStream_t st) {
-    const uint32_t tiles_m = (M + BM - 1) / BM;
-    const uint32_t tiles_n = (N + BN - 1) / BN;
-    const dim3 grid(tiles_m * tiles_n);
-    if (q)
-        hipLaunchKernelGGL(gemm_kernel<true>, grid, dim3(256), 0, st, (const uint16_t*)A,
-                           (const uint16_t*)nullptr, (const uint4*)q, (const uint16_t*)s,
-                           (const uint16_t*)b, C, M, N, K, G, out_bf16, tiles_m);
-    else
-        hipLaunchKernelGGL(gemm_kernel<false>, grid, dim3(256), 0, st, (const uint16_t*)A,
-                           (const uint16_t*)B, (const uint4*)nullptr, (const uint16_t*)nullptr,
-                           (const uint16_t*)nullptr, C, M, N, K, G, out_bf16, tiles_m);
-    return hipGetLastError();
+    // 256x128 tiles when they come in whole waves of 256 (one per CU),
+    // 128x128 otherwise.
+    const uint64_t big = (uint64_t)((M + 255) / 256) * ((N + 127) / 128);
+    int tile = (big >= 256 && big % 256 == 0) ? 0 : 1;
+    if (const char* e = getenv("MIORI_GEMM_TILE")) tile = atoi(e);
+    if (tile == 0) return launch_tile<256, 128>(A, B, q, s, b, C, M, N, K, G, out_bf16, st);
+    return launch_tile<128, 128>(A, B, q, s, b, C, M, N, K, G, out_bf16, st);
 }
 
 }  // namespace miori
