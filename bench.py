@@ -11,8 +11,8 @@ streams its weights from HBM. The K timed steps run as one HIP graph replay
 (back-to-back launches, no host in the loop), bracketed by synchronize and
 hipEvents on the launch stream.
 
-`roofline` reports the same kernel's average launch duration from a second
-replay with an event pair around every launch. The `gemm` object reports the
+`roofline` reports the same kernel's average launch duration over that
+replay (steps / event time), against the 8 TB/s HBM peak. The `gemm` object reports the
 bf16 prefill GEMM at M=1024, K=2048, N=8192 (34.36 GFLOP) against the dense
 bf16 MFMA peak. `cpu_baseline` times the CPU oracle (the reference's per-
 element dequant check loop, restated in C) on the same workload on the host.
@@ -47,86 +47,46 @@ def _parse():
 
 
 class Timer:
-    """Times a launch function over rotating operand sets with HIP graphs."""
+    """Times a launch function over rotating operand sets.
+
+    The timed steps are captured once into a HIP graph and replayed, so the
+    launches run back to back with no host in the loop; the time is taken
+    with hipEvents recorded on the launch stream around the replay, after a
+    device synchronize. steps/time is the per-launch average duration (it
+    agrees with rocprofv3's per-kernel average; see profiles/)."""
 
     def __init__(self, torch):
         self.torch = torch
 
-    def graph(self, fn, n, events=False):
-        torch = self.torch
-        g = torch.cuda.CUDAGraph()
-        evs = []
-        with torch.cuda.graph(g):
-            for i in range(n):
-                if events:
-                    e0 = torch.cuda.Event(enable_timing=True)
-                    e1 = torch.cuda.Event(enable_timing=True)
-                    e0.record()
-                    fn(i)
-                    e1.record()
-                    evs.append((e0, e1))
-                else:
-                    fn(i)
-        return g, evs
-
     def run(self, fn, steps, warmup):
-        """Return (total_ms for `steps` launches, mean per-launch ms, mode)."""
+        """Return (total_ms for `steps` launches, mode)."""
         torch = self.torch
         for i in range(warmup):
             fn(i)
         torch.cuda.synchronize()
-        mode = "hip-graph"
+        s0 = torch.cuda.Event(enable_timing=True)
+        s1 = torch.cuda.Event(enable_timing=True)
         try:
-            g, _ = self.graph(fn, steps)
-            g.replay()  # first replay uploads the graph
-            torch.cuda.synchronize()
-            s0 = torch.cuda.Event(enable_timing=True)
-            s1 = torch.cuda.Event(enable_timing=True)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for i in range(steps):
+                    fn(i)
+            g.replay()  # the first replay uploads the graph
             torch.cuda.synchronize()
             s0.record()
             g.replay()
             s1.record()
             torch.cuda.synchronize()
-            total = s0.elapsed_time(s1)
-            per = None
-            try:
-                g2, evs = self.graph(fn, steps, events=True)
-                g2.replay()
-                torch.cuda.synchronize()
-                g2.replay()
-                torch.cuda.synchronize()
-                per = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
-            except Exception as e:  # event nodes unsupported: fall back below
-                print(f"[bench] per-launch events in graph failed: {e}", file=sys.stderr)
-            if per is None or per <= 0:
-                per = self._eager_per_launch(fn, min(steps, 200))
-            return total, per, mode
-        except Exception as e:
+            return s0.elapsed_time(s1), "hip-graph"
+        except RuntimeError as e:
             print(f"[bench] graph capture failed ({e}); timing eager launches", file=sys.stderr)
-            mode = "eager"
-            s0 = torch.cuda.Event(enable_timing=True)
-            s1 = torch.cuda.Event(enable_timing=True)
-            torch.cuda.synchronize()
-            s0.record()
-            for i in range(steps):
-                fn(i)
-            s1.record()
-            torch.cuda.synchronize()
-            total = s0.elapsed_time(s1)
-            return total, self._eager_per_launch(fn, min(steps, 200)), mode
-
-    def _eager_per_launch(self, fn, n):
-        torch = self.torch
-        evs = []
-        for i in range(n):
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record()
-            fn(i)
-            b.record()
-            evs.append((a, b))
         torch.cuda.synchronize()
-        return sum(a.elapsed_time(b) for a, b in evs) / n
+        s0.record()
+        for i in range(steps):
+            fn(i)
+        s1.record()
+        torch.cuda.synchronize()
+        return s0.elapsed_time(s1), "eager"
 
 
 def gemv_case(torch, ops, synth, dev, bits, M, N, K, G, out_dtype, timer, steps, warmup):
@@ -151,7 +111,8 @@ def gemv_case(torch, ops, synth, dev, bits, M, N, K, G, out_dtype, timer, steps,
         else:
             fb(qs[j], ss[j], bs[j], x, y, N, K, M, group=G)
 
-    total, per, mode = timer.run(fn, steps, warmup)
+    total, mode = timer.run(fn, steps, warmup)
+    per = total / steps
     ybytes = M * N * (2 if out_dtype == torch.bfloat16 else 4)
     algo = wbytes + M * K * 2 + ybytes
     flops = 2.0 * M * N * K
@@ -191,7 +152,8 @@ def gemm_case(torch, ops, synth, oracle_mod, dev, M, N, K, fused, timer, steps, 
         def fn(i):
             ops.gemm_mpp(A, Bs[i % copies], C, M, N, K)
 
-    total, per, mode = timer.run(fn, steps, warmup)
+    total, mode = timer.run(fn, steps, warmup)
+    per = total / steps
     flops = 2.0 * M * N * K
     algo = wbytes + M * K * 2 + M * N * 2
     res = dict(M=M, N=N, K=K, fused=fused, copies=copies, mode=mode,

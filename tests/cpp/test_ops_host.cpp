@@ -1,0 +1,248 @@
+// C++ host test of the src/ops.h-signature wrappers (miori_amd/host):
+// a synthetic MLX-4bit safetensors file is written, loaded with Weights, and
+// the hot-path ops are called exactly as src/engine.cpp / src/main.cpp call
+// them (Metal&, encoder, Weights&, Tensor&, MTL::Buffer*). Results are
+// checked against the CPU oracle (oracle/cpu_ref.c) like the reference's
+// test_gemv (src/main.cpp:44-87), with the benchmark tolerance.
+//
+// Usage: test_ops_host <scratch-dir>     exit status 0 = all checks passed
+#include "../../miori_amd/host/ops_hip.h"
+#include "../../oracle/cpu_ref.h"
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+using namespace miori;
+
+namespace {
+
+int g_fail = 0;
+
+void expect(bool ok, const std::string& what) {
+    printf("%s %s\n", ok ? "PASS" : "FAIL", what.c_str());
+    if (!ok) ++g_fail;
+}
+
+uint64_t g_state = 0x4D494F52ull;
+uint64_t next64() {
+    uint64_t z = (g_state += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+double uni() { return (double)(next64() >> 11) * (1.0 / 9007199254740992.0); }
+
+struct Entry {
+    std::string name, dtype;
+    std::vector<int64_t> shape;
+    std::vector<uint8_t> bytes;
+};
+
+void write_safetensors(const std::string& path, const std::vector<Entry>& es) {
+    std::string h = "{\"__metadata__\":{\"format\":\"mlx\"}";
+    uint64_t off = 0;
+    for (const auto& e : es) {
+        h += ",\"" + e.name + "\":{\"dtype\":\"" + e.dtype + "\",\"shape\":[";
+        for (size_t i = 0; i < e.shape.size(); ++i) h += (i ? "," : "") + std::to_string(e.shape[i]);
+        h += "],\"data_offsets\":[" + std::to_string(off) + "," + std::to_string(off + e.bytes.size()) + "]}";
+        off += e.bytes.size();
+    }
+    h += "}";
+    while (h.size() % 8) h += ' ';
+    std::ofstream f(path, std::ios::binary);
+    const uint64_t n = h.size();
+    f.write((const char*)&n, 8);
+    f.write(h.data(), (std::streamsize)h.size());
+    for (const auto& e : es) f.write((const char*)e.bytes.data(), (std::streamsize)e.bytes.size());
+}
+
+// MLX-affine weights with the benchmark distributions.
+void quant(const std::string& base, int bits, int64_t N, int64_t K, int64_t G,
+           std::vector<Entry>& out) {
+    Entry q{base + ".weight", "U32", {N, K * bits / 32}, {}};
+    q.bytes.resize((size_t)N * K * bits / 8);
+    for (size_t i = 0; i < q.bytes.size(); i += 4) {
+        const uint32_t w = (uint32_t)(next64() >> 32);
+        memcpy(&q.bytes[i], &w, 4);
+    }
+    Entry s{base + ".scales", "BF16", {N, K / G}, {}}, b{base + ".biases", "BF16", {N, K / G}, {}};
+    s.bytes.resize((size_t)N * (K / G) * 2);
+    b.bytes.resize(s.bytes.size());
+    for (size_t i = 0; i < (size_t)N * (K / G); ++i) {
+        const float sc = bits == 4 ? (float)(0.001 + 0.009 * uni()) : (float)(1e-4 + 9e-4 * uni());
+        const uint16_t sb = orc_f32_to_bf16(sc);
+        const float sf = orc_bf16_to_f32(sb);
+        const float bi = bits == 4 ? (float)(-8.0 * sf + 1e-3 * (uni() - 0.5) * 3.4) : -128.f * sf;
+        const uint16_t bb = orc_f32_to_bf16(bi);
+        memcpy(&s.bytes[2 * i], &sb, 2);
+        memcpy(&b.bytes[2 * i], &bb, 2);
+    }
+    out.push_back(std::move(q));
+    out.push_back(std::move(s));
+    out.push_back(std::move(b));
+}
+
+// x[k] = ((37k mod 101) - 50) / 50, the reference test input (src/main.cpp:28)
+float xfn(size_t k) { return ((float)((k * 37) % 101) - 50.0f) / 50.0f; }
+
+bool close_enough(const float* got, const double* ref, size_t n, const char* what) {
+    double mref = 0, md = 0;
+    size_t ok2 = 0;
+    for (size_t i = 0; i < n; ++i) {
+        mref = std::max(mref, std::fabs(ref[i]));
+        const double d = std::fabs((double)got[i] - ref[i]);
+        md = std::max(md, d);
+        const double a = std::max(std::fabs(ref[i]), 1.1754943508222875e-38);
+        const double ulp = std::ldexp(1.0, (int)std::floor(std::log2(a)) - 7);
+        ok2 += d <= 2 * ulp;
+    }
+    const bool ok = md <= 1e-4 * mref && ok2 >= (size_t)std::ceil(0.999 * n);
+    printf("  %s: max|d|=%.3g max|ref|=%.3g within-2ulp=%.5f\n", what, md, mref, (double)ok2 / n);
+    return ok;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    const std::string dir = argc > 1 ? argv[1] : ".";
+    const std::string path = dir + "/test_ops_host.safetensors";
+    const int64_t N = 2048, K = 2048, G = 64, NV = 4096;
+    std::vector<Entry> es;
+    quant("layers.2.self_attn.q_proj", 4, N, K, G, es);
+    quant("embed_tokens", 8, NV, K, G, es);
+    write_safetensors(path, es);
+
+    Metal m;
+    std::string err;
+    if (!m.init("", err)) { printf("FAIL init: %s\n", err.c_str()); return 2; }
+    m.print_info();
+    Weights w;
+    if (!w.load(m, path, err)) { printf("FAIL load: %s\n", err.c_str()); return 2; }
+    expect(w.tensor_count() == 6, "safetensors loader: 6 tensors");
+    const Tensor& q = w.get("layers.2.self_attn.q_proj.weight");
+    const Tensor& s = w.get("layers.2.self_attn.q_proj.scales");
+    const Tensor& b = w.get("layers.2.self_attn.q_proj.biases");
+    expect(q.rows() == N && q.cols() * 8 == K && s.cols() == K / G, "tensor shapes");
+
+    // ---- gemv4, as test-gemv4 (src/main.cpp:44-87)
+    const int B = 16;
+    MTL::Buffer* x = m.new_buffer((size_t)B * K * 2);
+    MTL::Buffer* y = m.new_buffer((size_t)B * N * 4);
+    uint16_t* xp = (uint16_t*)x->contents();
+    for (int r = 0; r < B; ++r)
+        for (int64_t k = 0; k < K; ++k) xp[r * K + k] = orc_f32_to_bf16(xfn(k + 7 * r));
+    {
+        auto cb = m.begin();
+        auto e = cb->computeCommandEncoder();
+        gemv4(m, e, w, q, s, b, x, y, (uint32_t)N, (uint32_t)K);
+        e->endEncoding();
+        m.submit(cb, true);
+    }
+    std::vector<double> ref((size_t)B * N);
+    orc_gemv4_f64((const uint32_t*)q.ptr, (const uint16_t*)s.ptr, (const uint16_t*)b.ptr, xp,
+                  ref.data(), 1, N, K, G, 8);
+    expect(close_enough((const float*)y->contents(), ref.data(), N, "gemv4"), "gemv4 vs oracle");
+
+    // ---- gemv4_b with B = 4 (the reference's batch) and B = 16
+    for (int bb : {4, 16}) {
+        auto cb = m.begin();
+        auto e = cb->computeCommandEncoder();
+        gemv4_b(m, e, w, q, s, b, x, y, (uint32_t)N, (uint32_t)K, (uint32_t)bb);
+        m.submit(cb, true);
+        xp = (uint16_t*)x->contents();
+        orc_gemv4_f64((const uint32_t*)q.ptr, (const uint16_t*)s.ptr, (const uint16_t*)b.ptr, xp,
+                      ref.data(), bb, N, K, G, 8);
+        expect(close_enough((const float*)y->contents(), ref.data(), (size_t)bb * N, "gemv4_b"),
+               "gemv4_b B=" + std::to_string(bb));
+    }
+
+    // ---- gemv8 lm_head and gemv8_b_off on 4 rows at an offset
+    {
+        const Tensor& eq = w.get("embed_tokens.weight");
+        const Tensor& esc = w.get("embed_tokens.scales");
+        const Tensor& ebi = w.get("embed_tokens.biases");
+        MTL::Buffer* logits = m.new_buffer((size_t)8 * NV * 4);
+        auto cb = m.begin();
+        auto e = cb->computeCommandEncoder();
+        gemv8(m, e, w, eq, esc, ebi, x, logits, (uint32_t)NV, (uint32_t)K);
+        m.submit(cb, true);
+        xp = (uint16_t*)x->contents();
+        std::vector<double> r8((size_t)8 * NV);
+        orc_gemv8_f64((const uint32_t*)eq.ptr, (const uint16_t*)esc.ptr, (const uint16_t*)ebi.ptr,
+                      xp, r8.data(), 1, NV, K, G, 8);
+        expect(close_enough((const float*)logits->contents(), r8.data(), NV, "gemv8"), "gemv8 vs oracle");
+        cb = m.begin();
+        e = cb->computeCommandEncoder();
+        gemv8_b_off(m, e, w, eq, esc, ebi, x, logits, (uint32_t)NV, (uint32_t)K, 4,
+                    (uint32_t)(4 * K * 2), (uint32_t)(4 * NV * 4));
+        m.submit(cb, true);
+        xp = (uint16_t*)x->contents();
+        orc_gemv8_f64((const uint32_t*)eq.ptr, (const uint16_t*)esc.ptr, (const uint16_t*)ebi.ptr,
+                      xp + 4 * K, r8.data(), 4, NV, K, G, 8);
+        expect(close_enough((const float*)logits->contents() + 4 * NV, r8.data(), 4 * (size_t)NV,
+                            "gemv8_b_off"),
+               "gemv8_b_off rows 4..7");
+        logits->release();
+        delete logits;
+    }
+
+    // ---- weight cache + prefill GEMM, and the fused GEMM on the same operands
+    {
+        const uint32_t M = 96;
+        MTL::Buffer* cache = m.new_buffer((size_t)N * K * 2, false);
+        MTL::Buffer* A = m.new_buffer((size_t)M * K * 2);
+        MTL::Buffer* C1 = m.new_buffer((size_t)M * N * 4);
+        MTL::Buffer* C2 = m.new_buffer((size_t)M * N * 4);
+        uint16_t* ap = (uint16_t*)A->contents();
+        for (size_t i = 0; i < (size_t)M * K; ++i) ap[i] = orc_f32_to_bf16(sinf(0.13f * (float)i));
+        auto cb = m.begin();
+        auto e = cb->computeCommandEncoder();
+        dequant_tile(m, e, w, q, s, b, cache, (uint32_t)N, (uint32_t)K);
+        gemm_mpp(m, e, A, cache, C1, M, (uint32_t)N, (uint32_t)K);
+        gemm_q4(m, e, A, w, q, s, b, C2, M, (uint32_t)N, (uint32_t)K);
+        m.submit(cb, true);
+        std::vector<uint16_t> cache_host((size_t)N * K), cache_ref((size_t)N * K);
+        cache->download(cache_host.data(), cache_host.size() * 2);
+        orc_dequant4_bf16((const uint32_t*)q.ptr, (const uint16_t*)s.ptr, (const uint16_t*)b.ptr,
+                          cache_ref.data(), N, K, G);
+        expect(cache_host == cache_ref, "dequant_tile bit-exact vs oracle");
+        std::vector<int64_t> rows;
+        for (uint32_t r = 0; r < M; ++r) rows.push_back(r);
+        std::vector<double> cref((size_t)M * N);
+        ap = (uint16_t*)A->contents();
+        orc_gemm_bf16_f64(ap, cache_ref.data(), cref.data(), M, N, K, rows.data(), M, 8);
+        const float* c1 = (const float*)C1->contents();
+        const float* c2 = (const float*)C2->contents();
+        expect(close_enough(c1, cref.data(), (size_t)M * N, "gemm_mpp"), "gemm_mpp vs oracle");
+        expect(memcmp(c1, c2, (size_t)M * N * 4) == 0, "gemm_q4 bit-identical to dequant_tile + gemm_mpp");
+    }
+
+    // ---- errors surface as exceptions, as the reference's Metal::pso does
+    {
+        bool threw = false;
+        try {
+            auto cb = m.begin();
+            auto e = cb->computeCommandEncoder();
+            gemv4(m, e, w, q, s, b, x, y, (uint32_t)N * 2, (uint32_t)K);  // tensor too small
+        } catch (const std::runtime_error&) { threw = true; }
+        expect(threw, "out-of-range shape throws before launch");
+        threw = false;
+        try {
+            auto cb = m.begin();
+            auto e = cb->computeCommandEncoder();
+            gemv4_b(m, e, w, q, s, b, x, y, (uint32_t)N, (uint32_t)K, 40);  // B > 32
+        } catch (const std::runtime_error&) { threw = true; }
+        expect(threw, "batch of 40 rows is rejected");
+    }
+
+    x->release(); delete x;
+    y->release(); delete y;
+    std::remove(path.c_str());
+    printf("%s (%d failed)\n", g_fail ? "FAILED" : "ALL PASSED", g_fail);
+    return g_fail ? 1 : 0;
+}
