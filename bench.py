@@ -35,6 +35,19 @@ BF16_PEAK_TFLOPS = 2500.0
 ROTATE_BYTES = 1 << 30
 
 
+def measured_traffic():
+    """HBM bytes per launch of the headline GEMV, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes (scaled by a 256 MiB copy), or None."""
+    import re
+
+    path = os.path.join(ROOT, "profiles", "gemv4_k2048_n8192_hbm_traffic.md")
+    try:
+        m = re.search(r"gemv4_k2048_n8192_traffic_bytes=(\d+)", open(path).read())
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
 def _parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
@@ -43,6 +56,8 @@ def _parse():
     p.add_argument("--all", action="store_true", help="also time every benchmark config")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--calib-copy", action="store_true",
+                   help="also run a 256 MiB device copy (reference for the HBM byte counters)")
     return p.parse_args()
 
 
@@ -167,6 +182,52 @@ def gemm_case(torch, ops, synth, oracle_mod, dev, M, N, K, fused, timer, steps, 
     return res
 
 
+# One LFM-style layer's projections (name, K, N), BASELINE config 4.
+LAYER = [("q", 2048, 2048), ("k", 2048, 512), ("v", 2048, 512), ("o", 2048, 2048),
+         ("gate", 2048, 8192), ("up", 2048, 8192), ("down", 8192, 2048)]
+
+
+def chain_case(torch, ops, synth, dev, M, timer, layers=24, G=64, steps=3, warmup=1):
+    """Config 4: the fused 4-bit GEMM over a synthetic 24-layer projection
+    chain (7 projections per layer, distinct random weights per layer), M
+    activation rows. One step = the whole chain (168 GEMMs)."""
+    ws = []
+    for l in range(layers):
+        for i, (name, K, N) in enumerate(LAYER):
+            w = synth.quant_weights(N, K, G, 4, seed=synth.BASE_SEED + 1000 * l + i)
+            ws.append((ops.QuantLinear(w, dev), K, N))
+    a2 = ops.to_device_bits(synth.activations(M, 2048), dev)
+    a8 = ops.to_device_bits(synth.activations(M, 8192), dev)
+    outs = {N: torch.empty((M, N), dtype=torch.bfloat16, device=dev) for N in (512, 2048, 8192)}
+
+    def fn(i):
+        for lin, K, N in ws:
+            ops.gemm_q4(a8 if K == 8192 else a2, lin.q, lin.s, lin.b, outs[N], M, N, K, group=G)
+
+    total, mode = timer.run(fn, steps, warmup)
+    per = total / steps
+    flops = sum(2.0 * M * N * K for _, K, N in ws)
+    wbytes = sum(l.q.numel() * 4 + l.s.numel() * 2 + l.b.numel() * 2 for l, _, _ in ws)
+    res = dict(config=4, M=M, layers=layers, gemms=len(ws), mode=mode, us_per_chain=per * 1e3,
+               tflops=flops / (per * 1e-3) / 1e12, weight_gbs=wbytes / (per * 1e-3) / 1e9,
+               weight_bytes=wbytes, flops=flops)
+    res["mfma_frac"] = res["tflops"] / BF16_PEAK_TFLOPS
+    res["hbm_frac"] = res["weight_gbs"] / HBM_PEAK_GBS
+    del ws
+    torch.cuda.empty_cache()
+    return res
+
+
+def calib_copy(torch, dev):
+    """A plain 256 MiB device copy: reads and writes exactly 256 MiB, the
+    reference for scaling FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
 def cpu_baseline(seconds):
     """The oracle's faithful per-element GEMV (src/main.cpp:73-84 restated)
     on the headline workload, single-threaded, repeated for ~`seconds`."""
@@ -238,12 +299,15 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(head["gbs_kernel"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["gbs_kernel"] / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel_us": round(head["us_kernel"], 3)},
+                     "traffic": measured_traffic(), "kernel_us": round(head["us_kernel"], 3),
+                     "algorithmic_bytes": head["bytes"]},
         "gemm": {"workload": "bf16 GEMM M=1024 K=2048 N=8192, bf16 out",
                  "tflops": round(gemm["tflops_kernel"], 1),
                  "us": round(gemm["us_kernel"], 2),
                  "frac_of_bf16_peak": round(gemm["mfma_frac_kernel"], 4)},
     }
+    if args.calib_copy:
+        calib_copy(torch, dev)
     if args.all:
         out["configs"] = run_all(torch, ops, synth, oracle, dev, timer)
     if not args.no_cpu:
@@ -264,6 +328,9 @@ def run_all(torch, ops, synth, oracle, dev, timer):
     for M in (1, 8, 32):
         rows.append(dict(config=2, **gemv_case(torch, ops, synth, dev, 8, M, 131072, 2048, 64,
                                                torch.bfloat16, timer, 20, 3)))
+        print(f"[bench] {rows[-1]}", file=sys.stderr, flush=True)
+    for M in (1024, 32):
+        rows.append(chain_case(torch, ops, synth, dev, M, timer))
         print(f"[bench] {rows[-1]}", file=sys.stderr, flush=True)
     for fused in (False, True):
         for M in (256, 1024, 1472):
