@@ -42,8 +42,9 @@ int check_gemv(int bits, const void* q, const void* s, const void* b, const void
 hipError_t launch_batched(int bits, const void* q, const void* s, const void* b,
                           const void* x, void* y, uint32_t M, uint32_t N, uint32_t K,
                           uint32_t G, int out_bf16, hipStream_t st) {
-    if (M > 4 && gemv_mfma_supported(bits, M, K, G))
-        return launch_gemv_mfma(bits, q, s, b, x, y, M, N, K, G, out_bf16, st);
+    const int mode = bits == 4 ? 0 : 1;
+    if (M > 4 && skinny_supported(mode, M, N, K, G))
+        return launch_skinny(mode, x, q, s, b, y, M, N, K, G, out_bf16, st);
     return launch_gemv_valu(bits, q, s, b, x, y, M, N, K, G, out_bf16, st);
 }
 
@@ -122,6 +123,9 @@ int miori_gemm_bf16(const void* A, const void* B, void* C, uint32_t M, uint32_t 
     if (st) return st;
     if (!B) return MIORI_E_NULL;
     if (!aligned(B, 16)) return MIORI_E_ALIGN;
+    if (M <= 32 && skinny_supported(3, M, N, K, 64))
+        return hip_status(launch_skinny(3, A, B, nullptr, nullptr, C, M, N, K, 64,
+                                        out_dtype == MIORI_BF16, (hipStream_t)stream));
     return hip_status(launch_gemm(A, B, nullptr, nullptr, nullptr, C, M, N, K, 0,
                                   out_dtype == MIORI_BF16, (hipStream_t)stream));
 }
@@ -134,6 +138,11 @@ int miori_gemm_q4(const void* A, const void* q, const void* scales, const void* 
     if (!q || !scales || !biases) return MIORI_E_NULL;
     if (!(group == 32 || group == 64 || group == 128) || K % group != 0) return MIORI_E_SHAPE;
     if (!aligned(q, 16) || !aligned(scales, 2) || !aligned(biases, 2)) return MIORI_E_ALIGN;
+    // Small M runs on the skinny kernel, with the bf16 GEMM's routing (so the
+    // fused product stays bit-identical to dequant + bf16 GEMM).
+    if (M <= 32 && skinny_supported(2, M, N, K, group) && skinny_supported(3, M, N, K, 64))
+        return hip_status(launch_skinny(2, A, q, scales, biases, C, M, N, K, group,
+                                        out_dtype == MIORI_BF16, (hipStream_t)stream));
     return hip_status(launch_gemm(A, nullptr, q, scales, biases, C, M, N, K, group,
                                   out_dtype == MIORI_BF16, (hipStream_t)stream));
 }

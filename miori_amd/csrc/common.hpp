@@ -157,6 +157,52 @@ __device__ __forceinline__ int reduce_value(int RV, int i, int row) {
     return 2 * i + (row & 1) + ((row >> 1) ? H : 0);
 }
 
+// ---- direct-to-LDS DMA and barriers (gfx950)
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef const __attribute__((address_space(1))) void* gptr_t;
+
+__device__ __forceinline__ void dma16(const void* g, uint8_t* l) {
+    __builtin_amdgcn_global_load_lds((gptr_t)g, (lds_ptr_t)l, 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void* g, uint8_t* l) {
+    __builtin_amdgcn_global_load_lds((gptr_t)g, (lds_ptr_t)l, 4, 0, 0);
+}
+__device__ __forceinline__ void dma2(const void* g, uint8_t* l) {
+    __builtin_amdgcn_global_load_lds((gptr_t)g, (lds_ptr_t)l, 2, 0, 0);
+}
+
+// Workgroup barrier that neither waits for outstanding DMA (the fence of
+// __syncthreads would) nor lets the compiler move memory accesses across it.
+__device__ __forceinline__ void barrier_lds() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Cross-workgroup hand-off without C++ fences. Each XCD has its own L2, so a
+// device-scope release/acquire fence writes back and invalidates the whole
+// L2 (buffer_wbl2 / buffer_inv), microseconds per workgroup. Instead every
+// shared value is itself a device-coherent (relaxed, agent-scope) access,
+// and a producer drains its stores (vmcnt 0) before the counter RMW that
+// publishes them; the consumer issues its loads only after that RMW has
+// returned.
+__device__ __forceinline__ void st_shared_dev(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_shared_dev(const float* p) {
+    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t arrive_dev(uint32_t* ctr) {
+    return __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void reset_dev(uint32_t* ctr) {
+    __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+
 // Store one output element as fp32 or bf16.
 __device__ __forceinline__ void store_out(void* y, size_t idx, float v, bool bf16) {
     if (bf16)

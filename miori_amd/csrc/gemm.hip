@@ -38,35 +38,11 @@ namespace miori {
 
 namespace {
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-typedef const __attribute__((address_space(1))) void* gptr_t;
-
 constexpr int BK = 64;
 constexpr int ROWB = BK * 2;  // bytes per LDS row of a bf16 tile
 
 __device__ __forceinline__ uint32_t swz(uint32_t r, uint32_t kb) {
     return r * ROWB + ((kb ^ (r & 7u) ^ ((r >> 3) & 1u)) << 4);
-}
-
-__device__ __forceinline__ void dma16(const void* g, uint8_t* l) {
-    __builtin_amdgcn_global_load_lds((gptr_t)g, (lds_ptr_t)l, 16, 0, 0);
-}
-__device__ __forceinline__ void dma4(const void* g, uint8_t* l) {
-    __builtin_amdgcn_global_load_lds((gptr_t)g, (lds_ptr_t)l, 4, 0, 0);
-}
-__device__ __forceinline__ void dma2(const void* g, uint8_t* l) {
-    __builtin_amdgcn_global_load_lds((gptr_t)g, (lds_ptr_t)l, 2, 0, 0);
-}
-
-// Workgroup barrier that neither waits for outstanding DMA (the fence of
-// __syncthreads would) nor lets the compiler move memory accesses across it.
-__device__ __forceinline__ void barrier_lds() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 template <int BM, int BN, bool Q4, int G>

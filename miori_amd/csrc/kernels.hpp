@@ -29,4 +29,16 @@ hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* 
                        const void* b, void* C, uint32_t M, uint32_t N, uint32_t K,
                        uint32_t G, int out_bf16, hipStream_t st);
 
+// Skinny MFMA kernel (M <= 32), weight modes: 0 = 4-bit exact affine,
+// 1 = 8-bit exact affine, 2 = 4-bit dequantised to bf16 (fused GEMM),
+// 3 = bf16 weights.
+bool skinny_supported(int mode, uint32_t M, uint32_t N, uint32_t K, uint32_t G);
+hipError_t launch_skinny(int mode, const void* X, const void* W, const void* S, const void* B,
+                         void* Y, uint32_t M, uint32_t N, uint32_t K, uint32_t G, int out_bf16,
+                         hipStream_t st);
+
+// Split-K workspace of the stream (partials + zeroed completion counters).
+hipError_t workspace_get(hipStream_t st, size_t part_bytes, size_t n_counters, float** part,
+                         uint32_t** counters);
+
 }  // namespace miori

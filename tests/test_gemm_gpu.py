@@ -62,6 +62,7 @@ def _rows_for(M):
     (256, 8192, 2048), (1024, 8192, 2048), (1472, 8192, 2048),
     (256, 2048, 2560), (1024, 2048, 2560), (1472, 2048, 2560),
     (1, 64, 16), (23, 128, 80), (300, 192, 144), (64, 2048, 6144),
+    (32, 2048, 2048), (17, 512, 96), (8, 2560, 256), (32, 8192, 512),   # skinny path
 ])
 def test_gemm_bf16_parity(dev, M, K, N):
     say(f"gemm_bf16 M={M} K={K} N={N}")
@@ -79,6 +80,7 @@ def test_gemm_bf16_parity(dev, M, K, N):
 @pytest.mark.parametrize("M,K,N,G", [
     (1024, 2048, 8192, 64), (1472, 8192, 2048, 64), (256, 2048, 2560, 64),
     (32, 2048, 2048, 64), (32, 8192, 2048, 64), (100, 256, 48, 32), (64, 512, 128, 128),
+    (32, 2048, 8192, 64), (9, 1024, 80, 32), (20, 2048, 512, 128),      # skinny path
 ])
 def test_gemm_q4_fused_parity(dev, M, K, N, G):
     """Fused dequant-in-LDS GEMM: against the oracle, and bit-identical to the
@@ -100,17 +102,23 @@ def test_gemm_q4_fused_parity(dev, M, K, N, G):
     np.testing.assert_array_equal(ops.bits_of(C), ops.bits_of(C2))
 
 
-def test_gemm_tile_shape_consistency(dev):
-    """The reference's test-mpp-tile property (src/main.cpp:1403-1443): rows
-    0..22 of a 23-row product equal the same rows of the 64-row product."""
+@pytest.mark.parametrize("m_small,m_big", [(23, 32), (40, 64)])
+def test_gemm_tile_shape_consistency(dev, m_small, m_big):
+    """The reference's test-mpp-tile property (src/main.cpp:1403-1443): the
+    rows of a small-M product equal the same rows of a larger-M product.
+    It holds within each kernel family here, M <= 32 (skinny MFMA kernel)
+    and M > 32 (tiled GEMM); gemm_mpp32 and gemm_mpp are one entry point."""
     K, N = 2048, 6144
-    say("gemm 23 vs 64 rows")
-    w, Bbits, A = _operands(64, N, K, seed=4, dev=dev)
+    say(f"gemm {m_small} vs {m_big} rows")
+    w, Bbits, A = _operands(m_big, N, K, seed=4, dev=dev)
     Ad = ops.to_device_bits(A, dev)
     Bd = ops.to_device_bits(Bbits, dev)
-    C23 = torch.empty((23, N), dtype=torch.float32, device=dev)
-    C64 = torch.empty((64, N), dtype=torch.float32, device=dev)
-    ops.gemm_mpp32(Ad, Bd, C23, 23, N, K)
-    ops.gemm_mpp(Ad, Bd, C64, 64, N, K)
+    Cs = torch.empty((m_small, N), dtype=torch.float32, device=dev)
+    Cb = torch.empty((m_big, N), dtype=torch.float32, device=dev)
+    Cs2 = torch.empty((m_small, N), dtype=torch.float32, device=dev)
+    ops.gemm_mpp32(Ad, Bd, Cs, m_small, N, K)
+    ops.gemm_mpp(Ad, Bd, Cs2, m_small, N, K)
+    ops.gemm_mpp(Ad, Bd, Cb, m_big, N, K)
     torch.cuda.synchronize()
-    np.testing.assert_array_equal(C23.cpu().numpy(), C64[:23].cpu().numpy())
+    np.testing.assert_array_equal(Cs.cpu().numpy(), Cs2.cpu().numpy())
+    np.testing.assert_array_equal(Cs.cpu().numpy(), Cb[:m_small].cpu().numpy())

@@ -164,3 +164,17 @@ def test_gemv_rejects_bad_shapes(dev):
         yb = torch.empty(33 * 16, dtype=torch.float32, device=dev)
         xb = torch.zeros(33 * 256, dtype=torch.bfloat16, device=dev)
         ops.gemv4_b(lin.q, lin.s, lin.b, xb, yb, 16, 256, 33, group=64)
+
+
+@pytest.mark.parametrize("bits,M,N,K,G", [
+    (4, 8, 1000, 2048, 32), (4, 24, 640, 4096, 128), (4, 5, 96, 1024, 64),
+    (8, 12, 700, 2048, 32), (8, 32, 256, 4096, 128), (8, 6, 64, 512, 64),
+])
+def test_batched_skinny_groups(dev, bits, M, N, K, G):
+    """The MFMA (skinny) batched path with every group size and ragged N."""
+    say(f"gemv{bits}_b skinny M={M} N={N} K={K} G={G}")
+    w, lin = weights(N, K, G, bits, seed=M * 13 + N + G, dev=dev)
+    x, xd = acts(M, K, seed=M + 400, dev=dev)
+    y = _run(lin, xd, M, torch.float32)
+    ref = oracle.gemv_f64(w.q, w.s, w.b, x, bits, K, G, nthreads=NT)
+    check_close(y, ref, f"gemv{bits}_b M={M} G={G}")
