@@ -106,7 +106,7 @@ int miori_gemv_q8_batched(const void* q, const void* scales, const void* biases,
  * miori_dequant_q4_tile writes. Replaces gemm_mpp / gemm_mpp_off / gemm_mpp32
  * (src/ops.h:94-103, 207-209; kernels shaders/gemm_mpp.metal:36-73), whose B
  * is the Apple-MPP tile-major [N/64][K][64] layout.
- * Requires K % 64 == 0, N % 16 == 0, A and B 16-byte aligned. */
+ * Requires K % 64 == 0, N % 16 == 0, A, B and C 16-byte aligned. */
 int miori_gemm_bf16(const void* A, const void* B, void* C, uint32_t M,
                     uint32_t N, uint32_t K, int out_dtype, miori_stream stream);
 

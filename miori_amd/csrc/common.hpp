@@ -201,6 +201,18 @@ __device__ __forceinline__ uint32_t arrive_dev(uint32_t* ctr) {
 __device__ __forceinline__ void reset_dev(uint32_t* ctr) {
     __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// 16-byte device-coherent store / load (the sc1 form the compiler uses for
+// relaxed agent-scope atomics). The load's result may be used only after a
+// vmcnt wait; wait_then_use() ties a value to that wait.
+__device__ __forceinline__ void st_dev_x4(float* p, f32x4_t v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ f32x4_t ld_dev_x4(const float* p) {
+    f32x4_t v;
+    asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v) : "v"(p) : "memory");
+    return v;
+}
+__device__ __forceinline__ void wait_then_use(f32x4_t& v) { asm volatile("" : "+v"(v)); }
 
 
 // Store one output element as fp32 or bf16.

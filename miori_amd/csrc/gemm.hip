@@ -27,12 +27,14 @@
 //    results, bit for bit.
 //  * Workgroups are renumbered so each XCD (workgroup id mod 8) works on a
 //    contiguous block of output tiles and keeps its operand slabs in its own
-//    L2. The epilogue packs column pairs across lanes (DPP) for 4-byte bf16
-//    stores.
+//    L2. The epilogue stages the fp32 tile through LDS so every lane stores
+//    8 consecutive outputs (one 16-byte bf16 store).
 #include "common.hpp"
 #include "kernels.hpp"
 
 #include <stdlib.h>
+
+#include <type_traits>
 
 namespace miori {
 
@@ -70,6 +72,7 @@ struct Cfg {
     static constexpr int SB_INS = Q4 ? BN / 64 / 2 : 0;   // per wave (s or b), 64 rows each
     static constexpr int L = A_INS + B_INS + RAW_INS + SB_INS;
     static_assert(!Q4 || BN == 128, "fused dequant maps one thread per 32-code chunk");
+    static_assert(4 * WM * (WN + 8) * 4 <= LDS, "epilogue staging fits in the stage buffers");
 };
 
 template <int BM, int BN, bool Q4, int G>
@@ -77,7 +80,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
     const uint32_t* __restrict__ q, const uint16_t* __restrict__ s,
     const uint16_t* __restrict__ bsc, void* __restrict__ C, uint32_t M, uint32_t N,
-    uint32_t K, int out_bf16, uint32_t tiles_m, int remap) {
+    uint32_t K, int out_bf16, uint32_t tiles_m, int remap, float* __restrict__ part,
+    uint32_t SK, uint32_t ntiles) {
     using CF = Cfg<BM, BN, Q4, G>;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[CF::LDS];
 
@@ -88,9 +92,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     uint32_t pid = blockIdx.x;
     const uint32_t nwg = gridDim.x;
     if (remap && (nwg & 7u) == 0) pid = (pid & 7u) * (nwg >> 3) + (pid >> 3);
-    const uint32_t tm = pid % tiles_m, tn = pid / tiles_m;
+    // Split-K: workgroup pid computes K tiles [kt0, kt0 + KT) of output tile
+    // pid % ntiles; KT below counts this workgroup's tiles only.
+    const uint32_t tile = pid % ntiles, ksp = pid / ntiles;
+    const uint32_t tm = tile % tiles_m, tn = tile / tiles_m;
     const uint32_t m0 = tm * BM, n0 = tn * BN;
-    const uint32_t KT = K / BK;
+    const uint32_t KT_ALL = K / BK;
+    const uint32_t kt0 = KT_ALL * ksp / SK;
+    const uint32_t KT = KT_ALL * (ksp + 1) / SK - kt0;
     const uint32_t ng = Q4 ? K / G : 1;
 
     // Per-lane DMA source rows (clamped: rows past M / N load valid memory and
@@ -107,7 +116,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(
                 const uint32_t r = r0 + (lane >> 3);
                 const uint32_t kb = (lane & 7u) ^ (r & 7u) ^ ((r >> 3) & 1u);
                 const uint32_t row = min(m0 + r, M - 1u);
-                dma16(A + (size_t)row * K + kt * BK + kb * 8u,
+                dma16(A + (size_t)row * K + (kt0 + kt) * BK + kb * 8u,
                       lds + CF::A_OFF + stage_a * CF::A_ST + r0 * ROWB);
             }
         }
@@ -118,11 +127,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(
                 const uint32_t r = r0 + (lane >> 3);
                 const uint32_t kb = (lane & 7u) ^ (r & 7u) ^ ((r >> 3) & 1u);
                 const uint32_t row = min(n0 + r, N - 1u);
-                dma16(B + (size_t)row * K + kt * BK + kb * 8u, lds + CF::B_OFF + stage_b * CF::B_ST + r0 * ROWB);
+                dma16(B + (size_t)row * K + (kt0 + kt) * BK + kb * 8u, lds + CF::B_OFF + stage_b * CF::B_ST + r0 * ROWB);
             }
         } else {
             // raw codes of K tile kt (clamped to a valid tile): row r, chunk c at slot 2r + c
-            const uint32_t ktc = min(kr, KT - 1u);
+            const uint32_t ktc = kt0 + min(kr, KT - 1u);
             {
                 const uint32_t slot = wave * 64u + lane;
                 const uint32_t r = slot >> 1, c = slot & 1u;
@@ -142,6 +151,23 @@ __global__ __launch_bounds__(256) void gemm_kernel(
                 else
                     dma2(src + (size_t)row * ng + ktc * BK / G, dst);
             }
+        }
+    };
+
+    // bf16 path: DMA instruction p (0 <= p < L) of group kt into stage st, so
+    // a group can be spread over the MFMA stream.
+    auto issue_one = [&](uint32_t kt, uint32_t st, int p) {
+        const bool is_a = p < CF::A_INS;
+        const int pp = is_a ? p : p - CF::A_INS;
+        const uint32_t r0 = (wave * (is_a ? CF::A_INS : CF::B_INS) + pp) * 8u;
+        const uint32_t r = r0 + (lane >> 3);
+        const uint32_t kb = (lane & 7u) ^ (r & 7u) ^ ((r >> 3) & 1u);
+        if (is_a) {
+            const uint32_t row = min(m0 + r, M - 1u);
+            dma16(A + (size_t)row * K + (kt0 + kt) * BK + kb * 8u, lds + CF::A_OFF + st * CF::A_ST + r0 * ROWB);
+        } else {
+            const uint32_t row = min(n0 + r, N - 1u);
+            dma16(B + (size_t)row * K + (kt0 + kt) * BK + kb * 8u, lds + CF::B_OFF + st * CF::B_ST + r0 * ROWB);
         }
     };
 
@@ -213,13 +239,36 @@ __global__ __launch_bounds__(256) void gemm_kernel(
                 acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][i], bf[slot][j],
                                                                     acc[i][j], 0, 0, 0);
     };
+    // The MFMAs of one k-step with DMA instructions [P0, P1) of group dkt
+    // (stage dst) spread evenly between them: the wave issues each DMA while
+    // the matrix core is busy instead of stalling on a burst of them.
+    constexpr int NM = CF::TM * CF::TN;
+    constexpr int PER = (CF::L + 2) / 3;  // DMA instructions per k-step (k-steps 0..2)
+    static_assert(Q4 || PER <= NM, "one DMA per MFMA at most");
+    auto mfmas_dma = [&](int slot, bool dma, uint32_t dkt, uint32_t dst, auto p0c, auto p1c) {
+        constexpr int P0 = decltype(p0c)::value, P1 = decltype(p1c)::value;
+        constexpr int CNT = P1 - P0;
+#pragma unroll
+        for (int q = 0; q < NM; ++q) {
+            const int i = q / CF::TN, j = q % CF::TN;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][i], bf[slot][j],
+                                                                acc[i][j], 0, 0, 0);
+            if constexpr (CNT > 0) {
+                if ((q * CNT) / NM != ((q + 1) * CNT) / NM && dma)
+                    issue_one(dkt, dst, P0 + (q * CNT) / NM);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
 
     // Pipeline. Group p = {A(p), B(p)} (bf16) or {A(p), raw(p+1)} (fused; the
     // codes travel one group early and are dequantised two tiles ahead into a
-    // 3-deep bf16 ring). Groups 0..2 are issued up front; in step kt the
-    // barrier sits before the last k-step, where tile kt's LDS reads are done:
-    // it publishes group kt+1, frees stage kt % 3 for group kt+3, and the
-    // first fragments of tile kt+1 are read while the last MFMAs of kt run.
+    // 3-deep bf16 ring). In step kt the barrier sits before the last k-step,
+    // where tile kt's LDS reads are done: it publishes group kt+1, frees stage
+    // kt % 3, and the first fragments of tile kt+1 are read while the last
+    // MFMAs of kt run. Fused: groups 0..2 are issued up front and group kt+3
+    // right after the barrier of step kt. bf16: groups 0 and 1 up front, and
+    // group kt+2 interleaved with the MFMAs of tile kt.
     if constexpr (Q4) {
         issue(0, 0, 0, 0, false);  // raw(0)
         issue(0, 0, 1, 1, true);
@@ -233,99 +282,226 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     } else {
         issue(0, 0, 0, 0, true);
         if (KT > 1) issue(1, 1, 1, 1, true);
-        if (KT > 2) issue(2, 2, 2, 2, true);
-        if (KT > 2) wait_vm<2 * CF::L>(); else if (KT > 1) wait_vm<CF::L>(); else wait_vm<0>();
+        if (KT > 1) wait_vm<CF::L>(); else wait_vm<0>();
         barrier_lds();
     }
     read_frags(0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
 
-    for (uint32_t kt = 0; kt < KT; ++kt) {
+    if constexpr (Q4) {
+        for (uint32_t kt = 0; kt < KT; ++kt) {
 #pragma unroll
-        for (int ks = 0; ks < BK / 16 - 1; ++ks) {
-            read_frags(kt, ks + 1, (ks + 1) & 1);
-            asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(NFR) : "memory");  // k-step ks has landed
-            __builtin_amdgcn_sched_barrier(0);
-            mfmas(ks & 1);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if (kt + 1 < KT) {
-            if (kt + 2 < KT) wait_vm<CF::L>(); else wait_vm<0>();
-            barrier_lds();  // also completes the reads of the last k-step
-            if constexpr (Q4) {
+            for (int ks = 0; ks < BK / 16 - 1; ++ks) {
+                read_frags(kt, ks + 1, (ks + 1) & 1);
+                asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(NFR) : "memory");  // k-step ks has landed
+                __builtin_amdgcn_sched_barrier(0);
+                mfmas(ks & 1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (kt + 1 < KT) {
+                if (kt + 2 < KT) wait_vm<CF::L>(); else wait_vm<0>();
+                barrier_lds();  // also completes the reads of the last k-step
                 if (kt + 2 < KT) dequant_tile((kt + 2) % 3, (kt + 2) % 3);
                 if (kt + 3 < KT) issue(kt + 3, kt % 3, kt + 4, (kt + 4) % 3, true);
+                read_frags(kt + 1, 0, 0);
             } else {
-                if (kt + 3 < KT) issue(kt + 3, kt % 3, kt + 3, kt % 3, true);
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             }
-            read_frags(kt + 1, 0, 0);
-        } else {
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas((BK / 16 - 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        mfmas((BK / 16 - 1) & 1);
-        __builtin_amdgcn_sched_barrier(0);
+    } else {
+        // bf16: group kt+2 goes into stage (kt+2) % 3, freed by the barrier of
+        // step kt-1, spread over k-steps 0..2 of tile kt. The barrier of step
+        // kt then needs group kt+1, which is everything but the last L
+        // instructions.
+        for (uint32_t kt = 0; kt < KT; ++kt) {
+            const bool dma = kt + 2 < KT;
+            const uint32_t dkt = kt + 2, dst = (kt + 2) % 3;
+            using I0 = std::integral_constant<int, 0>;
+            read_frags(kt, 1, 1);
+            asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(NFR) : "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas_dma(0, dma, dkt, dst, I0{}, std::integral_constant<int, (PER < CF::L ? PER : CF::L)>{});
+            read_frags(kt, 2, 0);
+            asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(NFR) : "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas_dma(1, dma, dkt, dst, std::integral_constant<int, (PER < CF::L ? PER : CF::L)>{},
+                      std::integral_constant<int, (2 * PER < CF::L ? 2 * PER : CF::L)>{});
+            read_frags(kt, 3, 1);
+            asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(NFR) : "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas_dma(0, dma, dkt, dst, std::integral_constant<int, (2 * PER < CF::L ? 2 * PER : CF::L)>{},
+                      std::integral_constant<int, CF::L>{});
+            if (kt + 1 < KT) {
+                if (dma) wait_vm<CF::L>(); else wait_vm<0>();
+                barrier_lds();  // also completes the reads of the last k-step
+                read_frags(kt + 1, 0, 0);
+            } else {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
 
-    // Epilogue. Accumulator element e of lane l is row 8*(e/4) + 4*(l/32) + e%4,
-    // column l%32 of its 32x32 tile. For bf16 output, lanes 2p and 2p+1 swap
-    // one value each (DPP) so that each holds two adjacent columns of one row.
-    const bool odd = lane & 1u;
+    // Epilogue through LDS (the stage buffers are free once every wave is past
+    // the loop). Accumulator element e of lane l is row 8*(e/4) + 4*(l/32) +
+    // e%4, column l%32 of its 32x32 tile; each wave writes its WM x WN fp32
+    // tile to its own LDS region (row stride 72 floats: the two half-waves of
+    // a write land on disjoint banks), then reads it back 8 columns per lane
+    // and stores 16 bytes (bf16) or 2 x 16 bytes (fp32) per lane.
+    __syncthreads();
+    constexpr uint32_t RS = CF::WN + 8;  // floats per LDS row
+    float* ep = reinterpret_cast<float*>(lds) + wave * (CF::WM * RS);
 #pragma unroll
-    for (int i = 0; i < CF::TM; ++i) {
+    for (int i = 0; i < CF::TM; ++i)
 #pragma unroll
-        for (int j = 0; j < CF::TN; ++j) {
-            const uint32_t col = n0 + wn * CF::WN + j * 32 + (lane & 31u);
-            const uint32_t rbase = m0 + wm * CF::WM + i * 32 + 4u * (lane >> 5);
-            if (out_bf16) {
-                const uint32_t ce = col & ~1u;
+        for (int j = 0; j < CF::TN; ++j)
 #pragma unroll
-                for (int e = 0; e < 16; e += 2) {
-                    const float send = odd ? acc[i][j][e] : acc[i][j][e + 1];
-                    const float recv = dpp_f32<0xB1>(send);
-                    const float lo = odd ? recv : acc[i][j][e];
-                    const float hi = odd ? acc[i][j][e + 1] : recv;
-                    const uint32_t row = rbase + 8u * (e >> 2) + (e & 3) + (odd ? 1u : 0u);
-                    bf16x2_t p = {(__bf16)lo, (__bf16)hi};
-                    if (row < M && ce < N)
-                        *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(C) + (size_t)row * N + ce) =
-                            __builtin_bit_cast(uint32_t, p);
-                }
-            } else if (col < N) {
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const uint32_t row = rbase + 8u * (e >> 2) + (e & 3);
-                    if (row < M) reinterpret_cast<float*>(C)[(size_t)row * N + col] = acc[i][j][e];
-                }
+            for (int e = 0; e < 16; ++e) {
+                const uint32_t r = i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                ep[r * RS + j * 32 + (lane & 31u)] = acc[i][j][e];
             }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    constexpr uint32_t CPR = CF::WN / 8;          // 8-column chunks per row
+    constexpr uint32_t RPI = 64 / CPR;            // rows per pass
+    const uint32_t cc = lane % CPR, rr = lane / CPR;
+    const uint32_t col = n0 + wn * CF::WN + cc * 8u;
+    auto store8 = [&](uint32_t row, f32x4_t v0, f32x4_t v1) {
+        if (out_bf16) {
+            u32x4_t o;
+            bf16x2_t p0 = {(__bf16)v0[0], (__bf16)v0[1]}, p1 = {(__bf16)v0[2], (__bf16)v0[3]};
+            bf16x2_t p2 = {(__bf16)v1[0], (__bf16)v1[1]}, p3 = {(__bf16)v1[2], (__bf16)v1[3]};
+            o[0] = __builtin_bit_cast(uint32_t, p0);
+            o[1] = __builtin_bit_cast(uint32_t, p1);
+            o[2] = __builtin_bit_cast(uint32_t, p2);
+            o[3] = __builtin_bit_cast(uint32_t, p3);
+            *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(C) + (size_t)row * N + col) = o;
+        } else {
+            float* dst = reinterpret_cast<float*>(C) + (size_t)row * N + col;
+            *reinterpret_cast<f32x4_t*>(dst) = v0;
+            *reinterpret_cast<f32x4_t*>(dst + 4) = v1;
         }
+    };
+    if (SK == 1) {
+#pragma unroll 4
+        for (uint32_t r = rr; r < CF::WM; r += RPI) {
+            const uint32_t row = m0 + wm * CF::WM + r;
+            const f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u);
+            const f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u + 4u);
+            if (row < M && col < N) store8(row, v0, v1);
+        }
+        return;
+    }
+
+    // Split-K: the fp32 partial tile goes to part[ksp]; a second kernel adds
+    // the SK partials in split order (deterministic, and spread over every
+    // CU rather than funnelled through one workgroup per tile).
+    for (uint32_t r = rr; r < CF::WM; r += RPI) {
+        const uint32_t row = m0 + wm * CF::WM + r;
+        if (row >= M || col >= N) continue;
+        float* dst = part + ((size_t)ksp * M + row) * N + col;
+        *reinterpret_cast<f32x4_t*>(dst) = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u);
+        *reinterpret_cast<f32x4_t*>(dst + 4) = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u + 4u);
+    }
+}
+
+// out[i] = sum over k = 0..SK-1 of part[k][i], in that order; 8 outputs per
+// thread (M*N is a multiple of 16).
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part,
+                                                            void* __restrict__ C, size_t MN,
+                                                            uint32_t SK, int out_bf16) {
+    const size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    if (i >= MN) return;
+    constexpr uint32_t MAXSK = 16;
+    f32x4_t a[MAXSK][2];
+#pragma unroll
+    for (uint32_t k = 0; k < MAXSK; ++k)
+        if (k < SK) {
+            a[k][0] = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(part + k * MN + i));
+            a[k][1] = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(part + k * MN + i + 4));
+        }
+    f32x4_t v0 = {0.f, 0.f, 0.f, 0.f}, v1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (uint32_t k = 0; k < MAXSK; ++k)
+        if (k < SK) {
+            v0 += a[k][0];
+            v1 += a[k][1];
+        }
+    if (out_bf16) {
+        u32x4_t o;
+        bf16x2_t p0 = {(__bf16)v0[0], (__bf16)v0[1]}, p1 = {(__bf16)v0[2], (__bf16)v0[3]};
+        bf16x2_t p2 = {(__bf16)v1[0], (__bf16)v1[1]}, p3 = {(__bf16)v1[2], (__bf16)v1[3]};
+        o[0] = __builtin_bit_cast(uint32_t, p0);
+        o[1] = __builtin_bit_cast(uint32_t, p1);
+        o[2] = __builtin_bit_cast(uint32_t, p2);
+        o[3] = __builtin_bit_cast(uint32_t, p3);
+        *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(C) + i) = o;
+    } else {
+        *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(C) + i) = v0;
+        *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(C) + i + 4) = v1;
     }
 }
 
 template <int BM, int BN, bool Q4, int G>
 hipError_t launch_cfg(const void* A, const void* B, const void* q, const void* s, const void* b,
-                      void* C, uint32_t M, uint32_t N, uint32_t K, int out_bf16, hipStream_t st) {
+                      void* C, uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t SK,
+                      hipStream_t st) {
     const uint32_t tiles_m = (M + BM - 1) / BM;
     const uint32_t tiles_n = (N + BN - 1) / BN;
+    const uint32_t ntiles = tiles_m * tiles_n;
     const int remap = getenv("MIORI_GEMM_REMAP") ? atoi(getenv("MIORI_GEMM_REMAP")) : 1;
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, Q4, G>), dim3(tiles_m * tiles_n), dim3(256), 0, st,
+    float* part = nullptr;
+    uint32_t* counters = nullptr;
+    if (SK > 1) {
+        const hipError_t e = workspace_get(st, (size_t)SK * M * N * 4, 0, &part, &counters);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, Q4, G>), dim3(ntiles * SK), dim3(256), 0, st,
                        (const uint16_t*)A, (const uint16_t*)B, (const uint32_t*)q,
                        (const uint16_t*)s, (const uint16_t*)b, C, M, N, K, out_bf16, tiles_m,
-                       remap);
+                       remap, part, SK, ntiles);
+    if (SK > 1) {
+        const size_t MN = (size_t)M * N;
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((MN / 8 + 255) / 256)), dim3(256), 0,
+                           st, (const float*)part, C, MN, SK, out_bf16);
+    }
     return hipGetLastError();
 }
 
 template <int BM, int BN>
 hipError_t launch_tile(const void* A, const void* B, const void* q, const void* s, const void* b,
                        void* C, uint32_t M, uint32_t N, uint32_t K, uint32_t G, int out_bf16,
-                       hipStream_t st) {
-    if (!q) return launch_cfg<BM, BN, false, 64>(A, B, q, s, b, C, M, N, K, out_bf16, st);
+                       uint32_t SK, hipStream_t st) {
+    if (!q) return launch_cfg<BM, BN, false, 64>(A, B, q, s, b, C, M, N, K, out_bf16, SK, st);
     switch (G) {
-        case 32: return launch_cfg<BM, BN, true, 32>(A, B, q, s, b, C, M, N, K, out_bf16, st);
-        case 64: return launch_cfg<BM, BN, true, 64>(A, B, q, s, b, C, M, N, K, out_bf16, st);
-        case 128: return launch_cfg<BM, BN, true, 128>(A, B, q, s, b, C, M, N, K, out_bf16, st);
+        case 32: return launch_cfg<BM, BN, true, 32>(A, B, q, s, b, C, M, N, K, out_bf16, SK, st);
+        case 64: return launch_cfg<BM, BN, true, 64>(A, B, q, s, b, C, M, N, K, out_bf16, SK, st);
+        case 128: return launch_cfg<BM, BN, true, 128>(A, B, q, s, b, C, M, N, K, out_bf16, SK, st);
     }
     return hipErrorInvalidValue;
+}
+
+// K splits for `tiles` BM x BN output tiles of KT K tiles each, one
+// workgroup per CU at a time. Cost in half-K-tile units (a 64-deep K tile of
+// a 128x128 workgroup takes ~0.6 us): rounds of 256 workgroups x K tiles per
+// workgroup, plus for a split ~3 us of fixed cost and the partials' traffic
+// (SK*MN*4 bytes written and read back at ~5 TB/s, MN the padded output
+// size). A function of the tile grid and K only, so the fused and the
+// two-step products of one shape take the same path.
+uint32_t pick_split(uint32_t tiles, uint32_t KT, uint64_t MN) {
+    uint32_t best = 1;
+    uint64_t best_cost = 2ull * ((tiles + 255) / 256) * KT;
+    for (uint32_t sk = 2; sk <= 16 && KT / sk >= 4; ++sk) {
+        const uint64_t rounds = (tiles * (uint64_t)sk + 255) / 256;
+        const uint64_t traffic = sk * MN * 8 / 1500000;  // bytes / (5 TB/s * 0.3 us)
+        const uint64_t cost = 2 * rounds * ((KT + sk - 1) / sk) + 10 + traffic;
+        if (cost < best_cost) { best = sk; best_cost = cost; }
+    }
+    return best;
 }
 
 }  // namespace
@@ -333,13 +509,22 @@ hipError_t launch_tile(const void* A, const void* B, const void* q, const void* 
 hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* s,
                        const void* b, void* C, uint32_t M, uint32_t N, uint32_t K,
                        uint32_t G, int out_bf16, hipStream_t st) {
-    // 256x128 tiles when they come in whole waves of 256 (one per CU),
-    // 128x128 otherwise.
+    // 256x128 tiles when they come in whole waves of 256 (one per CU);
+    // otherwise 128x128 tiles with K split over workgroups to fill the chip.
     const uint64_t big = (uint64_t)((M + 255) / 256) * ((N + 127) / 128);
     int tile = (big >= 256 && big % 256 == 0) ? 0 : 1;
     if (const char* e = getenv("MIORI_GEMM_TILE")) tile = atoi(e);
-    if (tile == 0) return launch_tile<256, 128>(A, B, q, s, b, C, M, N, K, G, out_bf16, st);
-    return launch_tile<128, 128>(A, B, q, s, b, C, M, N, K, G, out_bf16, st);
+    const uint32_t ntiles = tile == 0 ? (uint32_t)big : ((M + 127) / 128) * ((N + 127) / 128);
+    // partial traffic from the padded tile grid, so every M in one row-tile
+    // count splits alike (rows of a small product equal those of a larger one)
+    const uint64_t tile_elems = tile == 0 ? 256 * 128 : 128 * 128;
+    uint32_t SK = pick_split(ntiles, K / 64, ntiles * tile_elems);
+    if (const char* e = getenv("MIORI_GEMM_SPLIT")) SK = (uint32_t)atoi(e);
+    if (SK < 1) SK = 1;
+    if (SK > 16) SK = 16;
+    if (SK > K / 64) SK = K / 64;
+    if (tile == 0) return launch_tile<256, 128>(A, B, q, s, b, C, M, N, K, G, out_bf16, SK, st);
+    return launch_tile<128, 128>(A, B, q, s, b, C, M, N, K, G, out_bf16, SK, st);
 }
 
 }  // namespace miori
