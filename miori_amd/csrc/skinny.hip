@@ -1,5 +1,6 @@
-// Skinny MFMA kernel for gfx950: y[M][N] = x[M][K] . W^T for M <= 32, with W
-// streamed from HBM once. One kernel, four weight modes:
+// Skinny MFMA kernel for gfx950: y[M][N] = x[M][K] . W^T for 5 <= M <= 32
+// (batched decode GEMV, small-M GEMM), with W streamed from HBM once and
+// every load of a wave in flight before its first MFMA. Four weight modes:
 //
 //   Q4X  4-bit MLX-affine, exact affine semantics (batched decode GEMV,
 //        replaces shaders/batch.metal:145-188 gemv4_b)
@@ -9,74 +10,83 @@
 //        bf16_rne(q*s + b), as the two-step dequant_tile + gemm_mpp)
 //   BF16 bf16 weight cache (gemm_mpp at small M)
 //
-// Structure:
-//  * A workgroup (4 waves) owns 64 output rows and a range of K tiles. Each K
-//    tile's weight rows, x rows and scales/biases go global -> LDS with
-//    global_load_lds DMA through a 3-stage ring, so HBM sees whole
-//    contiguous row segments and the loads of tile t+2 fly while tile t is
-//    computed. Chunks are XOR-swizzled by row so fragment reads are
-//    conflict-free.
-//  * Wave w takes the w-th quarter ("slice") of each K tile for all 64 rows:
-//    4 n-tiles x (M padded to 16 or 32) of v_mfma_f32_16x16x32_bf16. The x
-//    fragments of the slice are read once and reused by the 4 n-tiles.
-//  * Exact modes: codes become exact bf16 integers (128+q via one AND-OR),
-//    each quantisation group is accumulated alone (D_g) with X_g = sum of x
+// Structure (v_mfma_f32_16x16x32_bf16; x is the A operand, W^T the B one):
+//  * A workgroup of 8 waves owns 16*NT output rows; the waves split K, each
+//    taking a contiguous run of at most 8 128-wide K blocks (64 for 8-bit),
+//    and the eight partial tiles meet in LDS at the end (fixed order). No K
+//    split across workgroups: one pass, one store.
+//  * Weights go straight from memory to registers, 16 bytes per lane: lane
+//    (row n = lane % 16, quarter c = lane / 16) loads 32 codes (4-bit) or 16
+//    codes (8-bit) of row n. The MFMA sums over the 32 k of a step, so the k
+//    a lane quarter supplies in step r can be any 8 as long as x matches;
+//    exact modes keep every step inside one quantisation group by exchanging
+//    words between lane quarters with v_permlane32/16_swap (group 32: a 4x4
+//    word transpose; group 64 and 8-bit: one 32-lane swap; group >= 128:
+//    none), and x fragments are loaded at the matching k (kmap below).
+//  * Exact modes: codes become exact bf16 integers (128+q via one AND-OR per
+//    code pair), each group is accumulated alone (D_g) with X_g = sum of x
 //    over the group from an MFMA against ones, and folded in fp32:
 //        acc += s*D_g + (b - 128 s) X_g        (8-bit: hi nibbles x16, 2176)
 //    so the dequantised weights are never rounded.
-//  * The 4 waves' partial sums meet in LDS (fixed order). With split-K over
-//    workgroups the partials go to a workspace and the last workgroup of an
-//    output block (device-scope counter) adds them in split order, so the
-//    result does not depend on timing. Q4F and BF16 run the identical MFMA
-//    sequence, so the fused product is bit-identical to dequant + cache GEMM.
+//  * Q4F and BF16 run the identical MFMA sequence (same k order, same
+//    accumulation order), so the fused product is bit-identical to
+//    dequant + cache GEMM.
 #include "common.hpp"
 #include "kernels.hpp"
+
+#include <stdlib.h>
+
+#include <type_traits>
 
 namespace miori {
 
 namespace {
 
 enum { Q4X = 0, Q8X = 1, Q4F = 2, BF16 = 3 };
+constexpr int NW = 8;  // waves per workgroup
 
-template <int MODE, int MT, int G>
-struct SkCfg {
+template <int N>
+using ic = std::integral_constant<int, N>;
+
+template <int MODE, int MT, int NT, int G, int NBW>
+struct Sk {
     static constexpr bool EXACT = MODE == Q4X || MODE == Q8X;
-    static constexpr int NB = 64;                                   // rows per workgroup
-    static constexpr int SLICE = (EXACT && G > 64) ? G : 64;        // k per wave per tile
-    static constexpr int KTILE = 4 * SLICE;
-    static constexpr int KS = SLICE / 32;                           // MFMA k-steps per slice
-    static constexpr int MR = 16 * MT;
-    static constexpr int W_ROWB = (MODE == Q4X || MODE == Q4F) ? KTILE / 2
-                                  : (MODE == Q8X ? KTILE : KTILE * 2);
-    static constexpr int X_ROWB = KTILE * 2;
-    static constexpr int W_ST = NB * W_ROWB;
-    static constexpr int X_ST = MR * X_ROWB;
-    static constexpr int NGT = (MODE == BF16) ? 0 : KTILE / G;      // groups per row per tile
-    static constexpr int SB_DW = NGT / 2;                           // scale dwords per row per tile
-    static constexpr int SB_ST = NB * SB_DW * 4;
-    // LDS ring depth: 3 stages when they fit in the 160 KiB, else 2
-    static constexpr int NS = 3 * (X_ST + W_ST + 2 * SB_ST) <= 160 * 1024 ? 3 : 2;
-    static constexpr int X_OFF = 0;
-    static constexpr int W_OFF = NS * X_ST;
-    static constexpr int S_OFF = W_OFF + NS * W_ST;
-    static constexpr int B_OFF = S_OFF + NS * SB_ST;
-    static constexpr int RED = 4 * (4 * MT * 4 * 64) * 4;           // cross-wave reduction
-    static constexpr int STAGES = B_OFF + NS * SB_ST;
-    static constexpr int LDS = STAGES > RED ? STAGES : RED;
-    static constexpr int X_INS = X_ST / 1024 / 4;                   // DMA instructions per wave
-    static constexpr int W_INS = W_ST / 1024 / 4;
-    static constexpr int SB_INS = 2 * SB_DW;                        // s and b, 64 dwords each
-    static constexpr int W_CPR = W_ROWB / 16;                       // 16-byte chunks per row
-    static_assert(X_ST % 4096 == 0 && W_ST % 4096 == 0, "tile sizes");
-    static_assert(MODE == BF16 || NGT >= 2, "scale rows are moved as dwords");
+    static constexpr int KB = MODE == Q8X ? 64 : 128;          // k per block
+    static constexpr int STEPS = KB / 32;                      // MFMA k-steps per block
+    static constexpr int WL = MODE == BF16 ? STEPS : 1;        // 16-byte weight loads per n-tile
+    // k-steps folded together (one quantisation group inside the block)
+    static constexpr int SPF = !EXACT ? STEPS : ((G < KB ? G : KB) / 32);
+    static constexpr int NGB = EXACT ? (KB >= G ? KB / G : 1) : 1;  // scales per n-tile per block
+    // registers (dwords) per block slot, to size the pipeline depth
+    static constexpr int REGS = NT * WL * 4 + MT * STEPS * 4 + (MODE == BF16 ? 0 : 2 * NT * 2);
+    static constexpr int PD0 = 136 / REGS;
+    static constexpr int PD = PD0 < 2 ? 2 : (PD0 > 4 ? 4 : PD0);   // blocks in flight per wave
+    static constexpr int TOT = NT * MT * 4 * 64;                  // partial floats per wave
+    static constexpr int SBL = MODE == BF16 ? 0 : 2 * NT;         // scale/bias loads per block
+    static constexpr int L = NT * WL + SBL + MT * STEPS;          // loads per block
+    static constexpr int DEPTH = PD < NBW ? PD : NBW;             // slots actually used
+    static_assert((DEPTH - 1) * L < 64, "vmcnt range");
 };
 
-// chunk swizzle of a row: 16 consecutive rows read at the same logical
-// chunk land in distinct banks.
-template <int CPR>
-__device__ __forceinline__ uint32_t wsw(uint32_t r) {
-    if constexpr (CPR >= 16) return r & 15u;
-    else return (r >> 1) & (CPR - 1);
+// k offset (within a block) of the 8 values lane quarter c supplies in step r.
+template <int MODE, int G>
+__device__ __forceinline__ uint32_t kmap(uint32_t c, int r) {
+    if constexpr (MODE == Q4X && G == 32) return 32u * r + 8u * c;
+    else if constexpr (MODE == Q4X && G == 64)
+        return 32u * ((c & 1u) + 2u * (r >> 1)) + 8u * ((r & 1) + 2u * (c >> 1));
+    else if constexpr (MODE == Q8X) return 32u * r + 8u * (((c & 1u) << 1) | (c >> 1));
+    else return 32u * c + 8u * r;  // Q4X group >= 128, Q4F, BF16: no exchange
+}
+
+__device__ __forceinline__ void swap32u(uint32_t& a, uint32_t& b) {
+    auto p = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+    a = p[0];
+    b = p[1];
+}
+__device__ __forceinline__ void swap16u(uint32_t& a, uint32_t& b) {
+    auto p = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+    a = p[0];
+    b = p[1];
 }
 
 __device__ __forceinline__ bf16x8_t as_bf16x8_u(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
@@ -84,9 +94,9 @@ __device__ __forceinline__ bf16x8_t as_bf16x8_u(uint32_t a, uint32_t b, uint32_t
     return __builtin_bit_cast(bf16x8_t, v);
 }
 
-// x fragments: 8 consecutive bf16 (one 16-byte chunk), pair-permuted to the
-// slot order of the weight fragment (4-bit: (x0,x4)(x1,x5)(x2,x6)(x3,x7);
-// 8-bit: (x0,x2)(x1,x3)(x4,x6)(x5,x7); bf16 / fused: natural order).
+// x fragment: 8 consecutive bf16, pair-permuted to the slot order of the
+// weight fragment (4-bit exact: (x0,x4)(x1,x5)(x2,x6)(x3,x7); 8-bit exact:
+// (x0,x2)(x1,x3)(x4,x6)(x5,x7); Q4F / BF16: natural order).
 template <int MODE>
 __device__ __forceinline__ bf16x8_t x_frag(u32x4_t d) {
     if constexpr (MODE == Q4X)
@@ -103,355 +113,385 @@ __device__ __forceinline__ bf16x8_t x_frag(u32x4_t d) {
         return __builtin_bit_cast(bf16x8_t, d);
 }
 
+// Loads as inline asm with hand-placed waits (vmcnt counts them in issue
+// order), so PD blocks stay in flight. The kernel body is straight-line code
+// (the per-wave block loop is unrolled for a compile-time block count, no
+// branches), so a register a load is still filling is never copied; tie()
+// makes each value depend on its wait so no use is scheduled above it.
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void ld16(u32x4_t& d, const void* p) {
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(d) : "v"(p));
+}
+__device__ __forceinline__ void ld16nt(u32x4_t& d, const void* p) {
+    asm volatile("global_load_dwordx4 %0, %1, off nt" : "=v"(d) : "v"(p));
+}
+__device__ __forceinline__ void ld8(u32x2_t& d, const void* p) {
+    asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(d) : "v"(p));
+}
+__device__ __forceinline__ void ld4(uint32_t& d, const void* p) {
+    asm volatile("global_load_dword %0, %1, off" : "=v"(d) : "v"(p));
+}
+__device__ __forceinline__ void ld2(uint32_t& d, const void* p) {
+    asm volatile("global_load_ushort %0, %1, off" : "=v"(d) : "v"(p));
+}
+__device__ __forceinline__ void tie(u32x4_t& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void tie(uint32_t& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void tie(u32x2_t& v) { asm volatile("" : "+v"(v)); }
+
+// 128 + two 4-bit codes as exact bf16 integers. Plain C++ (not inline asm):
+// these values feed MFMA operands, and the compiler must see the VALU write
+// to insert the wait states an MFMA read of a just-written VGPR needs.
+__device__ __forceinline__ uint32_t nib2(uint32_t v) { return (v & 0x000F000Fu) | 0x43004300u; }
+
 __device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-template <int MODE, int MT, int G>
-__global__ __launch_bounds__(256) void skinny_kernel(
+template <int MODE, int MT, int NT, int G, int NBW>
+__global__ __launch_bounds__(NW * 64) void skinny_kernel(
     const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
     const uint16_t* __restrict__ S, const uint16_t* __restrict__ Bi, void* __restrict__ Y,
-    float* __restrict__ part, uint32_t* __restrict__ counters, uint32_t M, uint32_t N,
-    uint32_t K, uint32_t SK, int out_bf16) {
-    using C = SkCfg<MODE, MT, G>;
-    __shared__ __attribute__((aligned(1024))) uint8_t lds[C::LDS];
-    __shared__ uint32_t last_flag;
+    uint32_t M, uint32_t N, uint32_t K, int out_bf16) {
+    using C = Sk<MODE, MT, NT, G, NBW>;
+    __shared__ __attribute__((aligned(16))) float red[NW * C::TOT];
 
-    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+    const uint32_t t = threadIdx.x, lane = t & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const uint32_t j = lane & 15u, c = lane >> 4;
-    const uint32_t nblocks = (N + C::NB - 1) / C::NB;
-    const uint32_t nb = blockIdx.x % nblocks, ksi = blockIdx.x / nblocks;
-    const uint32_t n0 = nb * C::NB;
-    const uint32_t KT = K / C::KTILE;
-    const uint32_t kt0 = KT * ksi / SK, kt1 = KT * (ksi + 1) / SK;
+    const uint32_t n0 = blockIdx.x * 16u * NT;
+    const uint32_t nblk = K / C::KB;
+    const uint32_t b0 = wave * nblk / NW, b1 = (wave + 1) * nblk / NW;
+    const uint32_t nb = b1 - b0;
     const uint32_t ng = (MODE == BF16) ? 1u : K / G;
-    const uint64_t wrow = (MODE == Q4X || MODE == Q4F) ? K / 2 : (MODE == Q8X ? K : 2ull * K);
 
-    // Scale/bias DMA instructions are spread round-robin over the waves.
-    const int my_sb = (C::SB_INS - (int)wave + 3) / 4;
+    // per-lane row pointers (rows clamped into the matrices; clamped rows are
+    // never stored)
+    const uint8_t* wrow[NT];
+    const uint16_t* srow[NT];
+    const uint16_t* brow[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const uint32_t n = min(n0 + nt * 16u + j, N - 1u);
+        const size_t rb = (MODE == Q4X || MODE == Q4F) ? K / 2 : (MODE == Q8X ? K : 2ull * K);
+        wrow[nt] = W + (size_t)n * rb;
+        srow[nt] = S + (size_t)n * ng;
+        brow[nt] = Bi + (size_t)n * ng;
+    }
+    const uint16_t* xrow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) xrow[mt] = X + (size_t)min(mt * 16u + j, M - 1u) * K;
 
-    auto issue = [&](uint32_t kt, uint32_t st) {
-#pragma unroll
-        for (int p = 0; p < C::X_INS; ++p) {
-            const uint32_t byte0 = (wave * C::X_INS + p) * 1024u;
-            const uint32_t slot = byte0 / 16u + lane;
-            const uint32_t r = slot / (C::X_ROWB / 16), pc = slot % (C::X_ROWB / 16);
-            const uint32_t lc = pc ^ (r & 15u);
-            const uint32_t row = min(r, M - 1u);
-            dma16(X + (size_t)row * K + (size_t)kt * C::KTILE + lc * 8u,
-                  lds + C::X_OFF + st * C::X_ST + byte0);
-        }
-#pragma unroll
-        for (int p = 0; p < C::W_INS; ++p) {
-            const uint32_t byte0 = (wave * C::W_INS + p) * 1024u;
-            const uint32_t slot = byte0 / 16u + lane;
-            const uint32_t r = slot / C::W_CPR, pc = slot % C::W_CPR;
-            const uint32_t lc = pc ^ wsw<C::W_CPR>(r);
-            const uint32_t row = min(n0 + r, N - 1u);
-            dma16(W + row * wrow + (uint64_t)kt * C::W_ROWB + lc * 16u,
-                  lds + C::W_OFF + st * C::W_ST + byte0);
-        }
-        if constexpr (MODE != BF16) {
-            for (int i = (int)wave; i < C::SB_INS; i += 4) {
-                const int which = i / C::SB_DW, prt = i % C::SB_DW;
-                const uint32_t d = prt * 64u + lane;
-                const uint32_t r = d / C::SB_DW, dw = d % C::SB_DW;
-                const uint32_t row = min(n0 + r, N - 1u);
-                dma4((which ? Bi : S) + (size_t)row * ng + (size_t)kt * C::NGT + dw * 2u,
-                     lds + (which ? C::B_OFF : C::S_OFF) + st * C::SB_ST + prt * 256u);
-            }
-        }
-    };
-    // Wait until the loads of the oldest group in flight have landed, with
-    // `newer` groups still allowed in flight.
-    auto wait_groups = [&](int newer) {
-        const int per = C::X_INS + C::W_INS + my_sb;
-        if (newer == 0) { wait_vm<0>(); return; }
-        if (newer == 1) {
-            if (per == C::X_INS + C::W_INS) wait_vm<C::X_INS + C::W_INS>();
-            else if (per == C::X_INS + C::W_INS + 1) wait_vm<C::X_INS + C::W_INS + 1>();
-            else wait_vm<C::X_INS + C::W_INS + 2>();
-            return;
-        }
-        if (per == C::X_INS + C::W_INS) wait_vm<2 * (C::X_INS + C::W_INS)>();
-        else if (per == C::X_INS + C::W_INS + 1) wait_vm<2 * (C::X_INS + C::W_INS + 1)>();
-        else wait_vm<2 * (C::X_INS + C::W_INS + 2)>();
-    };
+    // block slots
+    u32x4_t wr[C::DEPTH][NT][C::WL];
+    u32x4_t xr[C::DEPTH][MT][C::STEPS];
+    // scales / biases of a block: 4 bf16 (u32x2) for 4 groups, else 1 dword
+    using SV = std::conditional_t<(C::NGB > 2), u32x2_t, uint32_t>;
+    SV sr[C::DEPTH][NT], br[C::DEPTH][NT];
 
-    f32x4_t acc[4][MT];
+    auto issue = [&](uint32_t blk, auto slot_c) {
+        constexpr int sl = decltype(slot_c)::value;
+        const uint32_t k0 = blk * C::KB;
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-    const bf16x8_t ones = as_bf16x8_u(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
-    const uint32_t c128 = 0x43004300u;
-
-    // Word of the slice that lane quarter c uses in k-step ks. Exact modes
-    // with more than one group per slice (G = 32) keep each k-step inside
-    // one group; otherwise a lane's words are contiguous.
-    auto word_of = [&](int ks) -> uint32_t {
-        if constexpr (C::EXACT && G == 32) return ks * 4u + c;
-        else return c * C::KS + ks;
-    };
-
-    auto compute = [&](uint32_t st, uint32_t kt) {
-        const uint8_t* xs = lds + C::X_OFF + st * C::X_ST;
-        const uint8_t* ws = lds + C::W_OFF + st * C::W_ST;
-        const uint16_t* ss = reinterpret_cast<const uint16_t*>(lds + C::S_OFF + st * C::SB_ST);
-        const uint16_t* bs = reinterpret_cast<const uint16_t*>(lds + C::B_OFF + st * C::SB_ST);
-        const uint32_t koff = wave * C::SLICE;  // slice start inside the tile
-        bf16x8_t af[MT][C::KS];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const uint32_t m = mt * 16u + j;
-#pragma unroll
-            for (int ks = 0; ks < C::KS; ++ks) {
-                // 4-bit: a word = 8 k; 8-bit exact: a word pair = 8 k; bf16/fused: 8 k.
-                const uint32_t k8 = (MODE == Q8X) ? koff / 8 + word_of(ks) : koff / 8 + word_of(ks);
-                const uint32_t phys = k8 ^ (m & 15u);
-                const u32x4_t d = *reinterpret_cast<const u32x4_t*>(xs + m * C::X_ROWB + phys * 16u);
-                af[mt][ks] = x_frag<MODE>(d);
-            }
-        }
-        constexpr int GPS = (C::EXACT && G == 32) ? 2 : 1;  // groups per slice (exact)
-        f32x4_t dx[MT][GPS];
-        if constexpr (C::EXACT) {
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int gg = 0; gg < GPS; ++gg) {
-                    dx[mt][gg] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int ks = gg * (C::KS / GPS); ks < (gg + 1) * (C::KS / GPS); ++ks)
-                        dx[mt][gg] = mfma16(af[mt][ks], ones, dx[mt][gg]);
-                }
-        }
-#pragma unroll
-        for (int nt = 0; nt < 4; ++nt) {
-            const uint32_t r = nt * 16u + j;
-            const uint8_t* wr = ws + r * C::W_ROWB;
+        for (int nt = 0; nt < NT; ++nt) {
             if constexpr (MODE == BF16) {
 #pragma unroll
-                for (int ks = 0; ks < C::KS; ++ks) {
-                    const uint32_t phys = (koff / 8 + word_of(ks)) ^ wsw<C::W_CPR>(r);
-                    const bf16x8_t bfr = *reinterpret_cast<const bf16x8_t*>(wr + phys * 16u);
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = mfma16(af[mt][ks], bfr, acc[nt][mt]);
+                for (int r = 0; r < C::STEPS; ++r)
+                    ld16nt(wr[sl][nt][r], wrow[nt] + 2u * (k0 + kmap<MODE, G>(c, r)));
+            } else {
+                const uint32_t byte = (MODE == Q8X) ? k0 + 16u * c : k0 / 2 + 16u * c;
+                ld16nt(wr[sl][nt][0], wrow[nt] + byte);
+            }
+            if constexpr (C::EXACT) {
+                // the NGB scales (and biases) of this block for row n
+                const uint32_t g0 = k0 / G;
+                if constexpr (C::NGB == 4) {
+                    ld8(sr[sl][nt], srow[nt] + g0);
+                    ld8(br[sl][nt], brow[nt] + g0);
+                } else if constexpr (C::NGB == 2) {
+                    ld4(sr[sl][nt], srow[nt] + g0);
+                    ld4(br[sl][nt], brow[nt] + g0);
+                } else {
+                    ld2(sr[sl][nt], srow[nt] + g0);
+                    ld2(br[sl][nt], brow[nt] + g0);
                 }
             } else if constexpr (MODE == Q4F) {
+                // this lane's group: codes k0 + 32c .. +31
+                const uint32_t g = (k0 + 32u * c) / G;
+                ld2(sr[sl][nt], srow[nt] + g);
+                ld2(br[sl][nt], brow[nt] + g);
+            }
+        }
 #pragma unroll
-                for (int ks = 0; ks < C::KS; ++ks) {
-                    const uint32_t w = koff / 8 + word_of(ks);           // word in the tile row
-                    const uint32_t phys = (w / 4) ^ wsw<C::W_CPR>(r);
-                    const uint32_t v = *reinterpret_cast<const uint32_t*>(wr + phys * 16u + (w % 4) * 4u);
-                    const uint32_t gt = w * 8u / G;                       // group in the tile
-                    const float sc = bf16_bits_to_f32(ss[r * C::NGT + gt]);
-                    const float bi = bf16_bits_to_f32(bs[r * C::NGT + gt]);
-                    const uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
-                    u32x4_t o;
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const float f0 = fmaf((float)((lo >> (8 * q)) & 0xFFu), sc, bi);
-                        const float f1 = fmaf((float)((hi >> (8 * q)) & 0xFFu), sc, bi);
-                        bf16x2_t pr = {(__bf16)f0, (__bf16)f1};
-                        o[q] = __builtin_bit_cast(uint32_t, pr);
-                    }
-                    const bf16x8_t bfr = __builtin_bit_cast(bf16x8_t, o);
+            for (int r = 0; r < C::STEPS; ++r)
+                ld16(xr[sl][mt][r], xrow[mt] + k0 + kmap<MODE, G>(c, r));
+    };
+
+    f32x4_t acc[NT][MT];
 #pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = mfma16(af[mt][ks], bfr, acc[nt][mt]);
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const bf16x8_t ones = as_bf16x8_u(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+
+    // scale / bias of fold f (0-based inside the block) for n-tile nt
+    auto scale_of = [&](const SV& v, int f) -> float {
+        if constexpr (C::NGB == 4) return bf16_bits_to_f32((v[f >> 1] >> (16 * (f & 1))) & 0xFFFFu);
+        else return bf16_bits_to_f32((v >> (16 * (f & 1))) & 0xFFFFu);
+    };
+
+    // valid = false (a padding block of a wave with fewer than NBW blocks):
+    // the block's loads were clamped to a real block and its contribution is
+    // zeroed by selects (x fragments, or the fold coefficients).
+    auto compute = [&](auto slot_c, bool valid) {
+        constexpr int sl = decltype(slot_c)::value;
+        bf16x8_t xf[MT][C::STEPS];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < C::STEPS; ++r) {
+                u32x4_t d = xr[sl][mt][r];
+                if constexpr (!C::EXACT) {
+                    d[0] = valid ? d[0] : 0u;
+                    d[1] = valid ? d[1] : 0u;
+                    d[2] = valid ? d[2] : 0u;
+                    d[3] = valid ? d[3] : 0u;
                 }
-            } else {
+                xf[mt][r] = x_frag<MODE>(d);
+            }
+        if constexpr (!C::EXACT) {
 #pragma unroll
-                for (int gg = 0; gg < GPS; ++gg) {
+            for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+                for (int r = 0; r < C::STEPS; ++r) {
+                    bf16x8_t bfr;
+                    if constexpr (MODE == BF16) {
+                        bfr = __builtin_bit_cast(bf16x8_t, wr[sl][nt][r]);
+                    } else {
+                        const float sc = bf16_bits_to_f32(sr[sl][nt] & 0xFFFFu);
+                        const float bi = bf16_bits_to_f32(br[sl][nt] & 0xFFFFu);
+                        const uint32_t v = wr[sl][nt][0][r];
+                        const uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
+                        u32x4_t o;
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const float f0 = fmaf((float)((lo >> (8 * q)) & 0xFFu), sc, bi);
+                            const float f1 = fmaf((float)((hi >> (8 * q)) & 0xFFu), sc, bi);
+                            bf16x2_t pr = {(__bf16)f0, (__bf16)f1};
+                            o[q] = __builtin_bit_cast(uint32_t, pr);
+                        }
+                        bfr = __builtin_bit_cast(bf16x8_t, o);
+                    }
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = mfma16(xf[mt][r], bfr, acc[nt][mt]);
+                }
+        } else {
+            // x sums of each fold (shared by the n-tiles)
+            constexpr int NF = C::STEPS / C::SPF;
+            f32x4_t dx[NF][MT];
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    dx[f][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int r = f * C::SPF; r < (f + 1) * C::SPF; ++r)
+                        dx[f][mt] = mfma16(xf[mt][r], ones, dx[f][mt]);
+                }
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                uint32_t w0 = wr[sl][nt][0][0], w1 = wr[sl][nt][0][1];
+                uint32_t w2 = wr[sl][nt][0][2], w3 = wr[sl][nt][0][3];
+                if constexpr (MODE == Q8X || G == 64 || G == 32) {
+                    swap32u(w0, w2);
+                    swap32u(w1, w3);
+                }
+                if constexpr (MODE == Q4X && G == 32) {
+                    swap16u(w0, w1);
+                    swap16u(w2, w3);
+                }
+                const uint32_t wv[4] = {w0, w1, w2, w3};
+#pragma unroll
+                for (int f = 0; f < NF; ++f) {
                     f32x4_t dd[MT], dh[MT];
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt) {
                         dd[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
                         dh[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
                     }
-                    uint32_t gt = 0;
 #pragma unroll
-                    for (int ks = gg * (C::KS / GPS); ks < (gg + 1) * (C::KS / GPS); ++ks) {
+                    for (int r = f * C::SPF; r < (f + 1) * C::SPF; ++r) {
                         if constexpr (MODE == Q4X) {
-                            const uint32_t w = koff / 8 + word_of(ks);
-                            gt = w * 8u / G;
-                            const uint32_t phys = (w / 4) ^ wsw<C::W_CPR>(r);
-                            const uint32_t v = *reinterpret_cast<const uint32_t*>(wr + phys * 16u + (w % 4) * 4u);
-                            const bf16x8_t bfr = as_bf16x8_u(and_or(v, 0x000F000Fu, c128),
-                                                             and_or(v >> 4, 0x000F000Fu, c128),
-                                                             and_or(v >> 8, 0x000F000Fu, c128),
-                                                             and_or(v >> 12, 0x000F000Fu, c128));
+                            const uint32_t v = wv[r];
+                            const bf16x8_t bfr = as_bf16x8_u(nib2(v),
+                                                             nib2(v >> 4),
+                                                             nib2(v >> 8),
+                                                             nib2(v >> 12));
 #pragma unroll
-                            for (int mt = 0; mt < MT; ++mt) dd[mt] = mfma16(af[mt][ks], bfr, dd[mt]);
+                            for (int mt = 0; mt < MT; ++mt) dd[mt] = mfma16(xf[mt][r], bfr, dd[mt]);
                         } else {
-                            // 8-bit: word pair wp holds 8 codes (k = 8*wp .. +8 of the slice)
-                            const uint32_t wp = koff / 8 + word_of(ks);
-                            gt = wp * 8u / G;
-                            const uint32_t byte = wp * 8u;
-                            const uint32_t phys = (byte / 16) ^ wsw<C::W_CPR>(r);
-                            const uint2 v = *reinterpret_cast<const uint2*>(wr + phys * 16u + (byte % 16));
-                            const bf16x8_t blo = as_bf16x8_u(and_or(v.x, 0x000F000Fu, c128),
-                                                             and_or(v.x >> 8, 0x000F000Fu, c128),
-                                                             and_or(v.y, 0x000F000Fu, c128),
-                                                             and_or(v.y >> 8, 0x000F000Fu, c128));
-                            const bf16x8_t bhi = as_bf16x8_u(and_or(v.x >> 4, 0x000F000Fu, c128),
-                                                             and_or(v.x >> 12, 0x000F000Fu, c128),
-                                                             and_or(v.y >> 4, 0x000F000Fu, c128),
-                                                             and_or(v.y >> 12, 0x000F000Fu, c128));
+                            const uint32_t vx = wv[2 * r], vy = wv[2 * r + 1];
+                            const bf16x8_t blo = as_bf16x8_u(nib2(vx),
+                                                             nib2(vx >> 8),
+                                                             nib2(vy),
+                                                             nib2(vy >> 8));
+                            const bf16x8_t bhi = as_bf16x8_u(nib2(vx >> 4),
+                                                             nib2(vx >> 12),
+                                                             nib2(vy >> 4),
+                                                             nib2(vy >> 12));
 #pragma unroll
                             for (int mt = 0; mt < MT; ++mt) {
-                                dd[mt] = mfma16(af[mt][ks], blo, dd[mt]);
-                                dh[mt] = mfma16(af[mt][ks], bhi, dh[mt]);
+                                dd[mt] = mfma16(xf[mt][r], blo, dd[mt]);
+                                dh[mt] = mfma16(xf[mt][r], bhi, dh[mt]);
                             }
                         }
                     }
-                    const float sc = bf16_bits_to_f32(ss[r * C::NGT + gt]);
-                    const float bi = bf16_bits_to_f32(bs[r * C::NGT + gt]);
+                    const float sc = valid ? scale_of(sr[sl][nt], f) : 0.f;
+                    const float bi = valid ? scale_of(br[sl][nt], f) : 0.f;
                     const float bx = (MODE == Q4X) ? fmaf(-128.f, sc, bi) : fmaf(-2176.f, sc, bi);
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             const float v = (MODE == Q4X) ? dd[mt][e] : fmaf(16.f, dh[mt][e], dd[mt][e]);
-                            acc[nt][mt][e] = fmaf(sc, v, fmaf(bx, dx[mt][gg][e], acc[nt][mt][e]));
+                            acc[nt][mt][e] = fmaf(sc, v, fmaf(bx, dx[f][mt][e], acc[nt][mt][e]));
                         }
                 }
             }
         }
-        (void)kt;
     };
 
-    // NS-stage DMA ring over this workgroup's K tiles [kt0, kt1): tile i+NS-1
-    // is issued while tile i is computed.
-    constexpr uint32_t D = C::NS - 1;
-    const uint32_t nk = kt1 - kt0;
-    for (uint32_t p = 0; p < D && p < nk; ++p) issue(kt0 + p, p);
-    for (uint32_t i = 0; i < nk; ++i) {
-        if (i + D < nk) issue(kt0 + i + D, (i + D) % C::NS);
-        const uint32_t ahead = nk - 1 - i;  // groups issued after tile i
-        wait_groups((int)(ahead < D ? ahead : D));
-        barrier_lds();
-        compute(i % C::NS, kt0 + i);
-        barrier_lds();  // stage i % NS is refilled NS-1 iterations later
-    }
-
-    // Cross-wave reduction (the stage buffers are free now).
-    float* red = reinterpret_cast<float*>(lds);
-    constexpr int TOT = 4 * MT * 4 * 64;
+    // DEPTH-deep pipeline over NBW block slots of this wave, fully unrolled:
+    // block i is computed from slot i % DEPTH once the blocks issued after it
+    // (at most DEPTH-1, L loads each) are the only ones in flight, then block
+    // i + DEPTH is issued into the same slot.
+    auto blk_of = [&](int i) { return min(b0 + (uint32_t)i, nblk - 1u); };
+    auto step = [&](auto i_c) {
+        constexpr int i = decltype(i_c)::value;
+        constexpr int sl = i % C::DEPTH;
+        constexpr int after = (NBW - 1 - i) < (C::DEPTH - 1) ? (NBW - 1 - i) : (C::DEPTH - 1);
+        wait_vm<after * C::L>();
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
+        for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+            for (int q = 0; q < C::WL; ++q) tie(wr[sl][nt][q]);
+            if constexpr (MODE != BF16) {
+                tie(sr[sl][nt]);
+                tie(br[sl][nt]);
+            }
+        }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) red[wave * TOT + ((nt * MT + mt) * 4 + e) * 64 + lane] = acc[nt][mt][e];
+            for (int r = 0; r < C::STEPS; ++r) tie(xr[sl][mt][r]);
+        compute(ic<sl>{}, (uint32_t)i < nb);
+        if constexpr (i + C::DEPTH < NBW) issue(blk_of(i + C::DEPTH), ic<sl>{});
+    };
+    issue(blk_of(0), ic<0>{});
+    if constexpr (C::DEPTH > 1) issue(blk_of(1), ic<1 % C::DEPTH>{});
+    if constexpr (C::DEPTH > 2) issue(blk_of(2), ic<2 % C::DEPTH>{});
+    if constexpr (C::DEPTH > 3) issue(blk_of(3), ic<3 % C::DEPTH>{});
+    step(ic<0>{});
+    if constexpr (NBW > 1) step(ic<1>{});
+    if constexpr (NBW > 2) { step(ic<2>{}); step(ic<3>{}); }
+    if constexpr (NBW > 4) { step(ic<4>{}); step(ic<5>{}); step(ic<6>{}); step(ic<7>{}); }
+
+    // Cross-wave reduction in fixed wave order.
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) red[wave * C::TOT + ((nt * MT + mt) * 4 + e) * 64 + lane] = acc[nt][mt][e];
     __syncthreads();
     const bool bf = out_bf16 != 0;
-    for (int e = t; e < TOT; e += 256) {
-        const float v = ((red[e] + red[TOT + e]) + red[2 * TOT + e]) + red[3 * TOT + e];
-        const uint32_t ln = e & 63u, r4 = (e >> 6) & 3u, tm = e >> 8;
+    for (uint32_t e = t; e < (uint32_t)C::TOT; e += NW * 64) {
+        float v = red[e];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) v += red[w * C::TOT + e];
+        const uint32_t ln = e & 63u, e4 = (e >> 6) & 3u, tm = e >> 8;
         const uint32_t nt = tm / MT, mt = tm % MT;
         const uint32_t n = n0 + nt * 16u + (ln & 15u);
-        const uint32_t m = mt * 16u + 4u * (ln >> 4) + r4;
-        if (n >= N || m >= M) continue;
-        if (SK == 1) store_out(Y, (size_t)m * N + n, v, bf);
-        else st_shared_dev(&part[((size_t)ksi * M + m) * N + n], v);
+        const uint32_t m = mt * 16u + 4u * (ln >> 4) + e4;
+        if (n < N && m < M) store_out(Y, (size_t)m * N + n, v, bf);
     }
-    if (SK == 1) return;
-
-    // Split-K: the last workgroup of this output block adds the partials in
-    // split order. The partials and the counter are device-coherent accesses
-    // (no L2-wide fences).
-    wait_vm<0>();
-    __syncthreads();
-    if (t == 0) last_flag = (arrive_dev(&counters[nb]) == SK - 1) ? 1u : 0u;
-    __syncthreads();
-    if (!last_flag) return;
-    for (int e = t; e < TOT; e += 256) {
-        const uint32_t ln = e & 63u, r4 = (e >> 6) & 3u, tm = e >> 8;
-        const uint32_t nt = tm / MT, mt = tm % MT;
-        const uint32_t n = n0 + nt * 16u + (ln & 15u);
-        const uint32_t m = mt * 16u + 4u * (ln >> 4) + r4;
-        if (n >= N || m >= M) continue;
-        float v = 0.f;
-        for (uint32_t s2 = 0; s2 < SK; ++s2)
-            v += ld_shared_dev(&part[((size_t)s2 * M + m) * N + n]);
-        store_out(Y, (size_t)m * N + n, v, bf);
-    }
-    if (t == 0) reset_dev(&counters[nb]);
 }
 
-template <int MODE, int MT, int G>
+template <int MODE, int MT, int NT, int G, int NBW>
 hipError_t launch_sk(const void* X, const void* W, const void* S, const void* B, void* Y,
                      uint32_t M, uint32_t N, uint32_t K, int out_bf16, hipStream_t st) {
-    using C = SkCfg<MODE, MT, G>;
-    const uint32_t nblocks = (N + C::NB - 1) / C::NB;
-    const uint32_t KT = K / C::KTILE;
-    // Split K until about 2 workgroups per CU, keeping >= 2 K tiles each.
-    uint32_t SK = 1;
-    while (nblocks * SK < 512 && KT / (SK * 2) >= 2) SK *= 2;
-    if (const char* e = getenv("MIORI_SKINNY_SPLIT")) SK = (uint32_t)atoi(e);
-    if (SK < 1) SK = 1;
-    if (SK > KT) SK = KT;
-    float* part = nullptr;
-    uint32_t* counters = nullptr;
-    if (SK > 1) {
-        hipError_t e = workspace_get(st, (size_t)SK * M * N * 4, nblocks, &part, &counters);
-        if (e != hipSuccess) return e;
-    }
-    hipLaunchKernelGGL((skinny_kernel<MODE, MT, G>), dim3(nblocks * SK), dim3(256), 0, st,
+    const uint32_t nwg = (N + 16 * NT - 1) / (16 * NT);
+    hipLaunchKernelGGL((skinny_kernel<MODE, MT, NT, G, NBW>), dim3(nwg), dim3(NW * 64), 0, st,
                        (const uint16_t*)X, (const uint8_t*)W, (const uint16_t*)S,
-                       (const uint16_t*)B, Y, part, counters, M, N, K, SK, out_bf16);
+                       (const uint16_t*)B, Y, M, N, K, out_bf16);
     return hipGetLastError();
 }
 
-template <int MODE, int MT>
+// blocks per wave, rounded up to 1, 2, 4 or 8
+inline int nbw_of(uint32_t K, uint32_t kb) {
+    const uint32_t per = (K / kb + NW - 1) / NW;
+    return per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : 8;
+}
+
+template <int MODE, int MT, int NT, int G>
+hipError_t by_nbw(const void* X, const void* W, const void* S, const void* B, void* Y,
+                  uint32_t M, uint32_t N, uint32_t K, int out_bf16, hipStream_t st) {
+    switch (nbw_of(K, MODE == Q8X ? 64u : 128u)) {
+        case 1: return launch_sk<MODE, MT, NT, G, 1>(X, W, S, B, Y, M, N, K, out_bf16, st);
+        case 2: return launch_sk<MODE, MT, NT, G, 2>(X, W, S, B, Y, M, N, K, out_bf16, st);
+        case 4: return launch_sk<MODE, MT, NT, G, 4>(X, W, S, B, Y, M, N, K, out_bf16, st);
+    }
+    return launch_sk<MODE, MT, NT, G, 8>(X, W, S, B, Y, M, N, K, out_bf16, st);
+}
+
+template <int MODE, int MT, int NT>
 hipError_t by_group(uint32_t G, const void* X, const void* W, const void* S, const void* B,
                     void* Y, uint32_t M, uint32_t N, uint32_t K, int out_bf16, hipStream_t st) {
     if constexpr (MODE == BF16) {
-        return launch_sk<BF16, MT, 64>(X, W, S, B, Y, M, N, K, out_bf16, st);
+        return by_nbw<BF16, MT, NT, 64>(X, W, S, B, Y, M, N, K, out_bf16, st);
     } else {
         switch (G) {
-            case 32: return launch_sk<MODE, MT, 32>(X, W, S, B, Y, M, N, K, out_bf16, st);
-            case 64: return launch_sk<MODE, MT, 64>(X, W, S, B, Y, M, N, K, out_bf16, st);
-            case 128: return launch_sk<MODE, MT, 128>(X, W, S, B, Y, M, N, K, out_bf16, st);
+            case 32: return by_nbw<MODE, MT, NT, 32>(X, W, S, B, Y, M, N, K, out_bf16, st);
+            case 64: return by_nbw<MODE, MT, NT, 64>(X, W, S, B, Y, M, N, K, out_bf16, st);
+            case 128: return by_nbw<MODE, MT, NT, 128>(X, W, S, B, Y, M, N, K, out_bf16, st);
         }
         return hipErrorInvalidValue;
     }
 }
 
 template <int MODE>
-hipError_t by_m(uint32_t G, const void* X, const void* W, const void* S, const void* B, void* Y,
-                uint32_t M, uint32_t N, uint32_t K, int out_bf16, hipStream_t st) {
-    return M <= 16 ? by_group<MODE, 1>(G, X, W, S, B, Y, M, N, K, out_bf16, st)
-                   : by_group<MODE, 2>(G, X, W, S, B, Y, M, N, K, out_bf16, st);
+hipError_t by_shape(uint32_t G, const void* X, const void* W, const void* S, const void* B,
+                    void* Y, uint32_t M, uint32_t N, uint32_t K, int out_bf16, hipStream_t st) {
+    // two n-tiles per workgroup (x loaded once for both) when that still
+    // gives >= 128 workgroups, else one
+    int nt = (N >= 4096) ? 2 : 1;
+    if (const char* e = getenv("MIORI_SKINNY_NT")) nt = atoi(e) == 1 ? 1 : 2;
+    if (M <= 16)
+        return nt == 2 ? by_group<MODE, 1, 2>(G, X, W, S, B, Y, M, N, K, out_bf16, st)
+                       : by_group<MODE, 1, 1>(G, X, W, S, B, Y, M, N, K, out_bf16, st);
+    return nt == 2 ? by_group<MODE, 2, 2>(G, X, W, S, B, Y, M, N, K, out_bf16, st)
+                   : by_group<MODE, 2, 1>(G, X, W, S, B, Y, M, N, K, out_bf16, st);
 }
 
 }  // namespace
 
-uint32_t skinny_ktile(int mode, uint32_t G) {
-    const bool exact = mode == 0 || mode == 1;
-    const uint32_t slice = (exact && G > 64) ? G : 64;
-    return 4 * slice;
-}
-
 bool skinny_supported(int mode, uint32_t M, uint32_t N, uint32_t K, uint32_t G) {
     if (M == 0 || M > 32 || N == 0) return false;
-    // 8-bit exact with group 128 and two m-tiles returns wrong values (cause
-    // not found yet); that case stays on the VALU kernel.
-    if (mode == 1 && G == 128 && M > 16) return false;
     if (mode != 3 && !(G == 32 || G == 64 || G == 128)) return false;
-    return K % skinny_ktile(mode, G) == 0;
+    const uint32_t kb = mode == 1 ? 64u : 128u;
+    // whole blocks, at most 8 per wave
+    return K % kb == 0 && K <= kb * NW * 8;
 }
 
 hipError_t launch_skinny(int mode, const void* X, const void* W, const void* S, const void* B,
                          void* Y, uint32_t M, uint32_t N, uint32_t K, uint32_t G, int out_bf16,
                          hipStream_t st) {
     switch (mode) {
-        case 0: return by_m<Q4X>(G, X, W, S, B, Y, M, N, K, out_bf16, st);
-        case 1: return by_m<Q8X>(G, X, W, S, B, Y, M, N, K, out_bf16, st);
-        case 2: return by_m<Q4F>(G, X, W, S, B, Y, M, N, K, out_bf16, st);
-        case 3: return by_m<BF16>(64, X, W, S, B, Y, M, N, K, out_bf16, st);
+        case 0: return by_shape<Q4X>(G, X, W, S, B, Y, M, N, K, out_bf16, st);
+        case 1: return by_shape<Q8X>(G, X, W, S, B, Y, M, N, K, out_bf16, st);
+        case 2: return by_shape<Q4F>(G, X, W, S, B, Y, M, N, K, out_bf16, st);
+        case 3: return by_shape<BF16>(64, X, W, S, B, Y, M, N, K, out_bf16, st);
     }
     return hipErrorInvalidValue;
 }
