@@ -37,13 +37,19 @@ int check_gemv(int bits, const void* q, const void* s, const void* b, const void
     return MIORI_OK;
 }
 
+// The skinny kernel DMAs each workgroup's scale / bias rows as 16-byte chunks.
+bool skinny_ok(int mode, uint32_t M, uint32_t N, uint32_t K, uint32_t G, const void* s,
+               const void* b) {
+    return skinny_supported(mode, M, N, K, G) && aligned(s, 16) && aligned(b, 16);
+}
+
 // Batched GEMV: the VALU kernel up to 4 rows (bit-identical to the single-row
 // product, as the reference's gemv4_b is), the MFMA kernel beyond.
 hipError_t launch_batched(int bits, const void* q, const void* s, const void* b,
                           const void* x, void* y, uint32_t M, uint32_t N, uint32_t K,
                           uint32_t G, int out_bf16, hipStream_t st) {
     const int mode = bits == 4 ? 0 : 1;
-    if (M > 4 && skinny_supported(mode, M, N, K, G))
+    if (M > 4 && skinny_ok(mode, M, N, K, G, s, b))
         return launch_skinny(mode, x, q, s, b, y, M, N, K, G, out_bf16, st);
     return launch_gemv_valu(bits, q, s, b, x, y, M, N, K, G, out_bf16, st);
 }
@@ -139,8 +145,9 @@ int miori_gemm_q4(const void* A, const void* q, const void* scales, const void* 
     if (!(group == 32 || group == 64 || group == 128) || K % group != 0) return MIORI_E_SHAPE;
     if (!aligned(q, 16) || !aligned(scales, 2) || !aligned(biases, 2)) return MIORI_E_ALIGN;
     // Small M runs on the skinny kernel, with the bf16 GEMM's routing (so the
-    // fused product stays bit-identical to dequant + bf16 GEMM).
-    if (M <= 32 && skinny_supported(2, M, N, K, group) && skinny_supported(3, M, N, K, 64))
+    // fused product stays bit-identical to dequant + bf16 GEMM; that needs
+    // K / group to be a multiple of 8 and 16-byte aligned scales / biases).
+    if (M <= 32 && skinny_ok(2, M, N, K, group, scales, biases) && skinny_supported(3, M, N, K, 64))
         return hip_status(launch_skinny(2, A, q, scales, biases, C, M, N, K, group,
                                         out_dtype == MIORI_BF16, (hipStream_t)stream));
     return hip_status(launch_gemm(A, nullptr, q, scales, biases, C, M, N, K, group,

@@ -56,14 +56,20 @@ struct Sk {
     static constexpr int WL = MODE == BF16 ? STEPS : 1;        // 16-byte weight loads per n-tile
     // k-steps folded together (one quantisation group inside the block)
     static constexpr int SPF = !EXACT ? STEPS : ((G < KB ? G : KB) / 32);
-    static constexpr int NGB = EXACT ? (KB >= G ? KB / G : 1) : 1;  // scales per n-tile per block
     // registers (dwords) per block slot, to size the pipeline depth
-    static constexpr int REGS = NT * WL * 4 + MT * STEPS * 4 + (MODE == BF16 ? 0 : 2 * NT * 2);
+    static constexpr int REGS = NT * WL * 4 + MT * STEPS * 4;
     static constexpr int PD0 = 136 / REGS;
     static constexpr int PD = PD0 < 2 ? 2 : (PD0 > 4 ? 4 : PD0);   // blocks in flight per wave
     static constexpr int TOT = NT * MT * 4 * 64;                  // partial floats per wave
-    static constexpr int SBL = MODE == BF16 ? 0 : 2 * NT;         // scale/bias loads per block
-    static constexpr int L = NT * WL + SBL + MT * STEPS;          // loads per block
+    static constexpr int L = NT * WL + MT * STEPS;                // loads per block
+    // scale / bias tiles of the workgroup's rows in LDS (all K/G groups of up
+    // to NBW * NW blocks), rounded up to whole 1 KiB DMA chunks
+    static constexpr int NB = 16 * NT;
+    static constexpr int NGMAX = EXACT || MODE == Q4F ? (NBW * NW * KB) / G : 0;
+    // (+ room for the masked reads of padding blocks past a row's end)
+    static constexpr int SB_BYTES = ((NB * NGMAX * 2 + NBW * KB / 16 + 1023) / 1024) * 1024;
+    static constexpr int RED_BYTES = NW * TOT * 4;
+    static constexpr int LDS = 2 * SB_BYTES > RED_BYTES ? 2 * SB_BYTES : RED_BYTES;
     static constexpr int DEPTH = PD < NBW ? PD : NBW;             // slots actually used
     static_assert((DEPTH - 1) * L < 64, "vmcnt range");
 };
@@ -153,7 +159,13 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
     const uint16_t* __restrict__ S, const uint16_t* __restrict__ Bi, void* __restrict__ Y,
     uint32_t M, uint32_t N, uint32_t K, int out_bf16) {
     using C = Sk<MODE, MT, NT, G, NBW>;
-    __shared__ __attribute__((aligned(16))) float red[NW * C::TOT];
+    // scale / bias tiles first, the cross-wave reduction buffer at the end
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[C::LDS];
+    float* red = reinterpret_cast<float*>(lds);
+    // LDS-typed pointers (ds_read, not flat loads that would wait on vmcnt)
+    typedef __attribute__((address_space(3))) const uint16_t* lds_u16;
+    const lds_u16 s_lds = (lds_u16)(lds);
+    const lds_u16 b_lds = (lds_u16)(lds + C::SB_BYTES);
 
     const uint32_t t = threadIdx.x, lane = t & 63u;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
@@ -167,15 +179,11 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
     // per-lane row pointers (rows clamped into the matrices; clamped rows are
     // never stored)
     const uint8_t* wrow[NT];
-    const uint16_t* srow[NT];
-    const uint16_t* brow[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
         const uint32_t n = min(n0 + nt * 16u + j, N - 1u);
         const size_t rb = (MODE == Q4X || MODE == Q4F) ? K / 2 : (MODE == Q8X ? K : 2ull * K);
         wrow[nt] = W + (size_t)n * rb;
-        srow[nt] = S + (size_t)n * ng;
-        brow[nt] = Bi + (size_t)n * ng;
     }
     const uint16_t* xrow[MT];
 #pragma unroll
@@ -184,9 +192,6 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
     // block slots
     u32x4_t wr[C::DEPTH][NT][C::WL];
     u32x4_t xr[C::DEPTH][MT][C::STEPS];
-    // scales / biases of a block: 4 bf16 (u32x2) for 4 groups, else 1 dword
-    using SV = std::conditional_t<(C::NGB > 2), u32x2_t, uint32_t>;
-    SV sr[C::DEPTH][NT], br[C::DEPTH][NT];
 
     auto issue = [&](uint32_t blk, auto slot_c) {
         constexpr int sl = decltype(slot_c)::value;
@@ -200,25 +205,6 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
             } else {
                 const uint32_t byte = (MODE == Q8X) ? k0 + 16u * c : k0 / 2 + 16u * c;
                 ld16nt(wr[sl][nt][0], wrow[nt] + byte);
-            }
-            if constexpr (C::EXACT) {
-                // the NGB scales (and biases) of this block for row n
-                const uint32_t g0 = k0 / G;
-                if constexpr (C::NGB == 4) {
-                    ld8(sr[sl][nt], srow[nt] + g0);
-                    ld8(br[sl][nt], brow[nt] + g0);
-                } else if constexpr (C::NGB == 2) {
-                    ld4(sr[sl][nt], srow[nt] + g0);
-                    ld4(br[sl][nt], brow[nt] + g0);
-                } else {
-                    ld2(sr[sl][nt], srow[nt] + g0);
-                    ld2(br[sl][nt], brow[nt] + g0);
-                }
-            } else if constexpr (MODE == Q4F) {
-                // this lane's group: codes k0 + 32c .. +31
-                const uint32_t g = (k0 + 32u * c) / G;
-                ld2(sr[sl][nt], srow[nt] + g);
-                ld2(br[sl][nt], brow[nt] + g);
             }
         }
 #pragma unroll
@@ -235,17 +221,27 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
         for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     const bf16x8_t ones = as_bf16x8_u(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
 
-    // scale / bias of fold f (0-based inside the block) for n-tile nt
-    auto scale_of = [&](const SV& v, int f) -> float {
-        if constexpr (C::NGB == 4) return bf16_bits_to_f32((v[f >> 1] >> (16 * (f & 1))) & 0xFFFFu);
-        else return bf16_bits_to_f32((v >> (16 * (f & 1))) & 0xFFFFu);
-    };
+    // scale / bias of this lane's row of n-tile nt, group (first group of the
+    // wave) + d: one LDS read at a per-n-tile base with an immediate offset d.
+    const uint32_t g_w0 = b0 * C::KB / G;
+    lds_u16 srl[NT];
+    lds_u16 brl[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        srl[nt] = s_lds + (nt * 16u + j) * ng + g_w0;
+        brl[nt] = b_lds + (nt * 16u + j) * ng + g_w0;
+    }
+    auto s_of = [&](int nt, int d) { return bf16_bits_to_f32(srl[nt][d]); };
+    auto b_of = [&](int nt, int d) { return bf16_bits_to_f32(brl[nt][d]); };
 
     // valid = false (a padding block of a wave with fewer than NBW blocks):
     // the block's loads were clamped to a real block and its contribution is
     // zeroed by selects (x fragments, or the fold coefficients).
-    auto compute = [&](auto slot_c, bool valid) {
-        constexpr int sl = decltype(slot_c)::value;
+    // block i (0-based in the wave) from slot i % DEPTH; group offsets inside
+    // the wave's groups are compile-time: (i*KB + k) / G
+    auto compute = [&](auto i_c, bool valid) {
+        constexpr int i = decltype(i_c)::value;
+        constexpr int sl = i % C::DEPTH;
         bf16x8_t xf[MT][C::STEPS];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
@@ -269,8 +265,10 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
                     if constexpr (MODE == BF16) {
                         bfr = __builtin_bit_cast(bf16x8_t, wr[sl][nt][r]);
                     } else {
-                        const float sc = bf16_bits_to_f32(sr[sl][nt] & 0xFFFFu);
-                        const float bi = bf16_bits_to_f32(br[sl][nt] & 0xFFFFu);
+                        // this lane's group: codes i*KB + 32c .. +31 of the wave's range
+                        const uint32_t d = (i * C::KB + 32u * c) / G;
+                        const float sc = bf16_bits_to_f32(srl[nt][d]);
+                        const float bi = bf16_bits_to_f32(brl[nt][d]);
                         const uint32_t v = wr[sl][nt][0][r];
                         const uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
                         u32x4_t o;
@@ -347,8 +345,10 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
                             }
                         }
                     }
-                    const float sc = valid ? scale_of(sr[sl][nt], f) : 0.f;
-                    const float bi = valid ? scale_of(br[sl][nt], f) : 0.f;
+                    const int d = (i * C::KB + f * C::SPF * 32) / G;
+                    const float sv = s_of(nt, d), bv = b_of(nt, d);
+                    const float sc = valid ? sv : 0.f;
+                    const float bi = valid ? bv : 0.f;
                     const float bx = (MODE == Q4X) ? fmaf(-128.f, sc, bi) : fmaf(-2176.f, sc, bi);
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt)
@@ -376,18 +376,31 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
         for (int nt = 0; nt < NT; ++nt) {
 #pragma unroll
             for (int q = 0; q < C::WL; ++q) tie(wr[sl][nt][q]);
-            if constexpr (MODE != BF16) {
-                tie(sr[sl][nt]);
-                tie(br[sl][nt]);
-            }
         }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int r = 0; r < C::STEPS; ++r) tie(xr[sl][mt][r]);
-        compute(ic<sl>{}, (uint32_t)i < nb);
+        if constexpr (i == 0 && MODE != BF16) barrier_lds();  // scale/bias tiles landed (all waves)
+        // keep each block's work (and its scale reads) inside its step
+        __builtin_amdgcn_sched_barrier(0);
+        compute(ic<i>{}, (uint32_t)i < nb);
         if constexpr (i + C::DEPTH < NBW) issue(blk_of(i + C::DEPTH), ic<sl>{});
+        __builtin_amdgcn_sched_barrier(0);
     };
+    // Scale / bias tiles of rows n0 .. n0+NB-1 (contiguous in S and B): 1 KiB
+    // DMA chunks spread over the waves, issued before the first block so the
+    // wait for block 0 covers them. Sources are clamped inside the arrays.
+    if constexpr (MODE != BF16) {
+        const uint32_t tb = C::NB * ng * 2u;                 // tile bytes
+        const size_t total = (size_t)N * ng * 2u;            // array bytes
+        const size_t base = (size_t)n0 * ng * 2u;
+        for (uint32_t q = wave; q * 1024u < tb; q += NW) {
+            const size_t off = min(base + q * 1024u + lane * 16u, total - 16u);
+            dma16(reinterpret_cast<const uint8_t*>(S) + off, lds + q * 1024u);
+            dma16(reinterpret_cast<const uint8_t*>(Bi) + off, lds + C::SB_BYTES + q * 1024u);
+        }
+    }
     issue(blk_of(0), ic<0>{});
     if constexpr (C::DEPTH > 1) issue(blk_of(1), ic<1 % C::DEPTH>{});
     if constexpr (C::DEPTH > 2) issue(blk_of(2), ic<2 % C::DEPTH>{});
@@ -397,7 +410,8 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
     if constexpr (NBW > 2) { step(ic<2>{}); step(ic<3>{}); }
     if constexpr (NBW > 4) { step(ic<4>{}); step(ic<5>{}); step(ic<6>{}); step(ic<7>{}); }
 
-    // Cross-wave reduction in fixed wave order.
+    // Cross-wave reduction in fixed wave order (the LDS tiles are dead).
+    __syncthreads();
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
@@ -480,7 +494,8 @@ bool skinny_supported(int mode, uint32_t M, uint32_t N, uint32_t K, uint32_t G) 
     if (M == 0 || M > 32 || N == 0) return false;
     if (mode != 3 && !(G == 32 || G == 64 || G == 128)) return false;
     const uint32_t kb = mode == 1 ? 64u : 128u;
-    // whole blocks, at most 8 per wave
+    // whole blocks, at most 8 per wave; scale rows in whole 16-byte chunks
+    if (mode != 3 && (K / G) % 8 != 0) return false;
     return K % kb == 0 && K <= kb * NW * 8;
 }
 

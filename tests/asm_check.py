@@ -42,9 +42,11 @@ def check_kernel(lines):
         for regs, at in pending:
             if regs & touched:
                 bad.append((ln, s, at))
-        if op.startswith(("global_load", "buffer_load")):
+        if op.startswith("global_load_lds") or (op.startswith("buffer_load") and " lds" in s):
+            pending.append((set(), ln))  # DMA into LDS: no destination VGPR
+        elif op.startswith(("global_load", "buffer_load", "flat_load")):
             pending.append((_regs(ops[0]), ln))
-        elif op.startswith(("global_store", "buffer_store", "global_atomic", "buffer_atomic")):
+        elif op.startswith(("global_store", "buffer_store", "global_atomic", "buffer_atomic", "flat_store", "flat_atomic")):
             pending.append((set(), ln))
     return bad
 
