@@ -144,10 +144,23 @@ __device__ __forceinline__ void tie(u32x4_t& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void tie(uint32_t& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void tie(u32x2_t& v) { asm volatile("" : "+v"(v)); }
 
-// 128 + two 4-bit codes as exact bf16 integers. Plain C++ (not inline asm):
-// these values feed MFMA operands, and the compiler must see the VALU write
-// to insert the wait states an MFMA read of a just-written VGPR needs.
-__device__ __forceinline__ uint32_t nib2(uint32_t v) { return (v & 0x000F000Fu) | 0x43004300u; }
+// 128 + two 4-bit codes as exact bf16 integers: (v & m) | c with m =
+// 0x000F000F in an SGPR and c = 0x43004300 in a VGPR, so the compiler can
+// select one v_and_or_b32 (this encoding takes no literal). The AND-OR itself
+// stays compiler code (not inline asm): its results feed MFMA operands and the
+// compiler must see the VALU write to insert the wait states an MFMA read of a
+// just-written VGPR needs. The two constants come from asm moves so they are
+// not folded back into literals.
+struct NibConst {
+    uint32_t m, c;
+};
+__device__ __forceinline__ NibConst nib_const() {
+    NibConst k;
+    asm volatile("s_mov_b32 %0, 0xf000f" : "=s"(k.m));
+    asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(k.c));
+    return k;
+}
+__device__ __forceinline__ uint32_t nib2(uint32_t v, NibConst k) { return (v & k.m) | k.c; }
 
 __device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -220,6 +233,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     const bf16x8_t ones = as_bf16x8_u(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+    const NibConst nk = nib_const();
 
     // scale / bias of this lane's row of n-tile nt, group (first group of the
     // wave) + d: one LDS read at a per-n-tile base with an immediate offset d.
@@ -322,22 +336,22 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
                     for (int r = f * C::SPF; r < (f + 1) * C::SPF; ++r) {
                         if constexpr (MODE == Q4X) {
                             const uint32_t v = wv[r];
-                            const bf16x8_t bfr = as_bf16x8_u(nib2(v),
-                                                             nib2(v >> 4),
-                                                             nib2(v >> 8),
-                                                             nib2(v >> 12));
+                            const bf16x8_t bfr = as_bf16x8_u(nib2(v, nk),
+                                                             nib2(v >> 4, nk),
+                                                             nib2(v >> 8, nk),
+                                                             nib2(v >> 12, nk));
 #pragma unroll
                             for (int mt = 0; mt < MT; ++mt) dd[mt] = mfma16(xf[mt][r], bfr, dd[mt]);
                         } else {
                             const uint32_t vx = wv[2 * r], vy = wv[2 * r + 1];
-                            const bf16x8_t blo = as_bf16x8_u(nib2(vx),
-                                                             nib2(vx >> 8),
-                                                             nib2(vy),
-                                                             nib2(vy >> 8));
-                            const bf16x8_t bhi = as_bf16x8_u(nib2(vx >> 4),
-                                                             nib2(vx >> 12),
-                                                             nib2(vy >> 4),
-                                                             nib2(vy >> 12));
+                            const bf16x8_t blo = as_bf16x8_u(nib2(vx, nk),
+                                                             nib2(vx >> 8, nk),
+                                                             nib2(vy, nk),
+                                                             nib2(vy >> 8, nk));
+                            const bf16x8_t bhi = as_bf16x8_u(nib2(vx >> 4, nk),
+                                                             nib2(vx >> 12, nk),
+                                                             nib2(vy >> 4, nk),
+                                                             nib2(vy >> 12, nk));
 #pragma unroll
                             for (int mt = 0; mt < MT; ++mt) {
                                 dd[mt] = mfma16(xf[mt][r], blo, dd[mt]);
@@ -474,18 +488,24 @@ hipError_t by_group(uint32_t G, const void* X, const void* W, const void* S, con
     }
 }
 
+// (an element's k order and wave reduction do not depend on NT)
+template <int MODE, int MT>
+hipError_t by_nt(int nt, uint32_t G, const void* X, const void* W, const void* S, const void* B,
+                 void* Y, uint32_t M, uint32_t N, uint32_t K, int out_bf16, hipStream_t st) {
+    if (nt >= 2) return by_group<MODE, MT, 2>(G, X, W, S, B, Y, M, N, K, out_bf16, st);
+    return by_group<MODE, MT, 1>(G, X, W, S, B, Y, M, N, K, out_bf16, st);
+}
+
 template <int MODE>
 hipError_t by_shape(uint32_t G, const void* X, const void* W, const void* S, const void* B,
                     void* Y, uint32_t M, uint32_t N, uint32_t K, int out_bf16, hipStream_t st) {
-    // two n-tiles per workgroup (x loaded once for both) when that still
-    // gives >= 128 workgroups, else one
-    int nt = (N >= 4096) ? 2 : 1;
-    if (const char* e = getenv("MIORI_SKINNY_NT")) nt = atoi(e) == 1 ? 1 : 2;
-    if (M <= 16)
-        return nt == 2 ? by_group<MODE, 1, 2>(G, X, W, S, B, Y, M, N, K, out_bf16, st)
-                       : by_group<MODE, 1, 1>(G, X, W, S, B, Y, M, N, K, out_bf16, st);
-    return nt == 2 ? by_group<MODE, 2, 2>(G, X, W, S, B, Y, M, N, K, out_bf16, st)
-                   : by_group<MODE, 2, 1>(G, X, W, S, B, Y, M, N, K, out_bf16, st);
+    // n-tiles per workgroup: x is loaded once per workgroup and reused by
+    // each n-tile; two while that still gives >= 256 workgroups (more rows
+    // per workgroup measured slower: fewer workgroups in flight)
+    int nt = (N >= 8192) ? 2 : 1;
+    if (const char* e = getenv("MIORI_SKINNY_NT")) nt = atoi(e) >= 2 ? 2 : 1;
+    if (M <= 16) return by_nt<MODE, 1>(nt, G, X, W, S, B, Y, M, N, K, out_bf16, st);
+    return by_nt<MODE, 2>(nt, G, X, W, S, B, Y, M, N, K, out_bf16, st);
 }
 
 }  // namespace

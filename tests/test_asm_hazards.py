@@ -2,6 +2,7 @@
 assembly: no register of a pending load is read or reused early (such a read
 gives wrong values; a reuse as an address faults the GPU)."""
 import os
+import re
 import shutil
 import subprocess
 
@@ -32,7 +33,14 @@ def test_skinny_kernel_waits(tmp_path):
            "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S", "-I", CSRC,
            "-o", str(out), os.path.join(CSRC, "skinny.hip")]
     subprocess.run(cmd, check=True, capture_output=True, timeout=600)
-    res = check_file(out.read_text(), "skinny_kernel")
+    text = out.read_text()
+    res = check_file(text, "skinny_kernel")
     assert len(res) >= 100, "expected every skinny_kernel instantiation"
     bad = {k: v for k, v in res.items() if v}
     assert not bad, {k[:80]: v[:3] for k, v in bad.items()}
+    # no register spills: a spill is a copy, and copying a register an inline
+    # asm load is still filling reads garbage
+    names = re.findall(r"\.name:\s+(_Z\S*skinny_kernel\S*)", text)
+    scratch = re.findall(r"\.name:\s+(\S+)(?:(?!\.name:).)*?\.private_segment_fixed_size:\s+(\d+)", text, re.S)
+    spilled = [n for n, sz in scratch if "skinny_kernel" in n and int(sz) > 0]
+    assert names and not spilled, spilled[:5]
