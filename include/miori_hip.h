@@ -120,6 +120,16 @@ int miori_gemm_q4(const void* A, const void* q, const void* scales,
                   const void* biases, void* C, uint32_t M, uint32_t N, uint32_t K,
                   uint32_t group, int out_dtype, miori_stream stream);
 
+/* Strided GEMM for any shape: C[m*ldc + n] = sum_k A[m*lda + k] * B[n*ldb + k],
+ * bf16 operands, fp32 output, each output one fp32 FMA chain over k = 0..K-1
+ * (the reference kernel's accumulation). The fallback for shapes the MFMA
+ * GEMM does not take. Replaces gemm_naive (src/ops.h:30-32, kernel
+ * shaders/ops.metal:199-251); byte offsets are applied by the caller.
+ * Requires lda >= K, ldb >= K, ldc >= N; A and B 2-byte, C 4-byte aligned. */
+int miori_gemm_naive(const void* A, const void* B, float* C, uint32_t M, uint32_t N,
+                     uint32_t K, uint32_t lda, uint32_t ldb, uint32_t ldc,
+                     miori_stream stream);
+
 /* ---- weight-cache builders ----------------------------------------------
  * out = bf16(float(code)*scale + bias), RNE, bit-exact with the CPU dequant.
  * dequant_q4_tile writes the layout miori_gemm_bf16 reads (row-major [N][K]);

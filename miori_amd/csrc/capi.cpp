@@ -154,6 +154,14 @@ int miori_gemm_q4(const void* A, const void* q, const void* scales, const void* 
                                   out_dtype == MIORI_BF16, (hipStream_t)stream));
 }
 
+int miori_gemm_naive(const void* A, const void* B, float* C, uint32_t M, uint32_t N,
+                     uint32_t K, uint32_t lda, uint32_t ldb, uint32_t ldc, miori_stream stream) {
+    if (!A || !B || !C) return MIORI_E_NULL;
+    if (M == 0 || N == 0 || K == 0 || lda < K || ldb < K || ldc < N) return MIORI_E_SHAPE;
+    if (!aligned(A, 2) || !aligned(B, 2) || !aligned(C, 4)) return MIORI_E_ALIGN;
+    return hip_status(launch_gemm_naive(A, B, C, M, N, K, lda, ldb, ldc, (hipStream_t)stream));
+}
+
 static int dequant_common(int bits, const void* q, const void* s, const void* b, void* out,
                           uint32_t N, uint32_t K, uint32_t G, hipStream_t st) {
     if (!q || !s || !b || !out) return MIORI_E_NULL;

@@ -182,37 +182,6 @@ __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// Cross-workgroup hand-off without C++ fences. Each XCD has its own L2, so a
-// device-scope release/acquire fence writes back and invalidates the whole
-// L2 (buffer_wbl2 / buffer_inv), microseconds per workgroup. Instead every
-// shared value is itself a device-coherent (relaxed, agent-scope) access,
-// and a producer drains its stores (vmcnt 0) before the counter RMW that
-// publishes them; the consumer issues its loads only after that RMW has
-// returned.
-__device__ __forceinline__ void st_shared_dev(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_shared_dev(const float* p) {
-    return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t arrive_dev(uint32_t* ctr) {
-    return __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void reset_dev(uint32_t* ctr) {
-    __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// 16-byte device-coherent store / load (the sc1 form the compiler uses for
-// relaxed agent-scope atomics). The load's result may be used only after a
-// vmcnt wait; wait_then_use() ties a value to that wait.
-__device__ __forceinline__ void st_dev_x4(float* p, f32x4_t v) {
-    asm volatile("global_store_dwordx4 %0, %1, off sc1" ::"v"(p), "v"(v) : "memory");
-}
-__device__ __forceinline__ f32x4_t ld_dev_x4(const float* p) {
-    f32x4_t v;
-    asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v) : "v"(p) : "memory");
-    return v;
-}
-__device__ __forceinline__ void wait_then_use(f32x4_t& v) { asm volatile("" : "+v"(v)); }
 
 
 // Store one output element as fp32 or bf16.

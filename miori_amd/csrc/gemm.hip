@@ -455,9 +455,8 @@ hipError_t launch_cfg(const void* A, const void* B, const void* q, const void* s
     const uint32_t ntiles = tiles_m * tiles_n;
     const int remap = getenv("MIORI_GEMM_REMAP") ? atoi(getenv("MIORI_GEMM_REMAP")) : 1;
     float* part = nullptr;
-    uint32_t* counters = nullptr;
     if (SK > 1) {
-        const hipError_t e = workspace_get(st, (size_t)SK * M * N * 4, 0, &part, &counters);
+        const hipError_t e = workspace_get(st, (size_t)SK * M * N * 4, &part);
         if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL((gemm_kernel<BM, BN, Q4, G>), dim3(ntiles * SK), dim3(256), 0, st,

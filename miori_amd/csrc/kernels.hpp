@@ -13,11 +13,6 @@ hipError_t launch_gemv_valu(int bits, const void* q, const void* s, const void* 
                             uint32_t G, int out_bf16, hipStream_t st);
 void gemv_split(int bits, uint32_t K, uint32_t* S, int* cpl);
 
-bool gemv_mfma_supported(int bits, uint32_t M, uint32_t K, uint32_t G);
-// Batched GEMV on MFMA (exact affine dequant, per-group fp32 scaling), M <= 32.
-hipError_t launch_gemv_mfma(int bits, const void* q, const void* s, const void* b,
-                            const void* x, void* y, uint32_t M, uint32_t N, uint32_t K,
-                            uint32_t G, int out_bf16, hipStream_t st);
 
 // bf16 -> row-major bf16 dequant.
 hipError_t launch_dequant(int bits, const void* q, const void* s, const void* b, void* out,
@@ -29,6 +24,12 @@ hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* 
                        const void* b, void* C, uint32_t M, uint32_t N, uint32_t K,
                        uint32_t G, int out_bf16, hipStream_t st);
 
+// C (fp32, row stride ldc) = A . B^T for any shape, bf16 operands with row
+// strides lda / ldb; one sequential fp32 FMA chain over k per output.
+hipError_t launch_gemm_naive(const void* A, const void* B, float* C, uint32_t M, uint32_t N,
+                             uint32_t K, uint32_t lda, uint32_t ldb, uint32_t ldc,
+                             hipStream_t st);
+
 // Skinny MFMA kernel (M <= 32), weight modes: 0 = 4-bit exact affine,
 // 1 = 8-bit exact affine, 2 = 4-bit dequantised to bf16 (fused GEMM),
 // 3 = bf16 weights.
@@ -37,8 +38,7 @@ hipError_t launch_skinny(int mode, const void* X, const void* W, const void* S, 
                          void* Y, uint32_t M, uint32_t N, uint32_t K, uint32_t G, int out_bf16,
                          hipStream_t st);
 
-// Split-K workspace of the stream (partials + zeroed completion counters).
-hipError_t workspace_get(hipStream_t st, size_t part_bytes, size_t n_counters, float** part,
-                         uint32_t** counters);
+// Split-K partials workspace of the current device (grown outside graph capture).
+hipError_t workspace_get(hipStream_t st, size_t bytes, float** part);
 
 }  // namespace miori

@@ -211,6 +211,20 @@ void gemm_mpp_off(Metal&, MTL::ComputeCommandEncoder* e, MTL::Buffer* A, MTL::Bu
           "gemm_mpp");
 }
 
+void gemm_naive(Metal&, MTL::ComputeCommandEncoder* e, MTL::Buffer* A, MTL::Buffer* B,
+                MTL::Buffer* C, uint32_t M, uint32_t N, uint32_t K, uint32_t lda, uint32_t ldb,
+                uint32_t ldc, uint32_t aoff, uint32_t boff, uint32_t coff) {
+    if (M == 0 || N == 0 || K == 0) throw std::runtime_error("gemm_naive: empty shape");
+    need(A, aoff, ((uint64_t)(M - 1) * lda + K) * 2, "A");
+    need(B, boff, ((uint64_t)(N - 1) * ldb + K) * 2, "B");
+    need(C, coff, ((uint64_t)(M - 1) * ldc + N) * 4, "C");
+    e->use_in(A); e->use_in(B);
+    e->use_out(C);
+    check(miori_gemm_naive(at(A, aoff), at(B, boff), (float*)at_w(C, coff), M, N, K, lda, ldb,
+                           ldc, e->stream()),
+          "gemm_naive");
+}
+
 void gemm_mpp(Metal& m, MTL::ComputeCommandEncoder* e, MTL::Buffer* A, MTL::Buffer* B,
               MTL::Buffer* C, uint32_t M, uint32_t N, uint32_t K, uint32_t boff) {
     gemm_mpp_off(m, e, A, B, C, M, N, K, 0, boff, 0);

@@ -43,6 +43,11 @@ void dequant4(Metal& m, MTL::ComputeCommandEncoder* e, const Weights& w,
 void dequant_tile(Metal& m, MTL::ComputeCommandEncoder* e, const Weights& w,
                   const Tensor& q, const Tensor& s, const Tensor& b,
                   MTL::Buffer* out, uint32_t N, uint32_t K, uint32_t boff = 0);
+// src/ops.h:30-32 (fallback GEMM for any shape; fp32 C, strided operands)
+void gemm_naive(Metal& m, MTL::ComputeCommandEncoder* e, MTL::Buffer* A,
+                MTL::Buffer* B, MTL::Buffer* C, uint32_t M, uint32_t N, uint32_t K,
+                uint32_t lda, uint32_t ldb, uint32_t ldc,
+                uint32_t aoff = 0, uint32_t boff = 0, uint32_t coff = 0);
 // src/ops.h:94-96
 void gemm_mpp(Metal& m, MTL::ComputeCommandEncoder* e, MTL::Buffer* A,
               MTL::Buffer* B, MTL::Buffer* C, uint32_t M, uint32_t N, uint32_t K,

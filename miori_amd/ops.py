@@ -138,6 +138,23 @@ def gemm_q4(A, q, s, b, C, M, N, K, group=64, stream=None):
               _stream(stream))
 
 
+def gemm_naive(A, B, C, M, N, K, lda, ldb, ldc, aoff=0, boff=0, coff=0, stream=None):
+    """C[m*ldc + n] = sum_k A[m*lda + k] * B[n*ldb + k] for any shape, bf16
+    operands, fp32 C, one sequential fp32 FMA chain per output (src/ops.h:30-32;
+    shaders/ops.metal:199-251). aoff / boff / coff are byte offsets into the
+    tensors, as the reference's buffer offsets are."""
+    if C.dtype != torch.float32:
+        raise ValueError("gemm_naive writes float32")
+    for name, off, align in (("aoff", aoff, 2), ("boff", boff, 2), ("coff", coff, 4)):
+        if off < 0 or off % align:
+            raise ValueError(f"{name} must be a non-negative multiple of {align}")
+    ap = _ptr(A, "A", aoff + ((M - 1) * lda + K) * 2)
+    bp = _ptr(B, "B", boff + ((N - 1) * ldb + K) * 2)
+    cp = _ptr(C, "C", coff + ((M - 1) * ldc + N) * 4)
+    _lib.call("miori_gemm_naive", ap + aoff, bp + boff, cp + coff, M, N, K, lda, ldb, ldc,
+              _stream(stream))
+
+
 def _dequant(fn, bits, q, s, b, out, N, K, group, stream):
     if K % group:
         raise MioriError(fn, -2, "K must be a multiple of the group size")

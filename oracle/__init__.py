@@ -53,6 +53,7 @@ def _load():
         for name in ("orc_gemv4_rows_f64", "orc_gemv8_rows_f64"):
             getattr(lib, name).argtypes = [P, P, P, P, P, I, I, I, I, I, I, ctypes.c_int]
         lib.orc_gemm_bf16_f64.argtypes = [P, P, P, I, I, I, P, I, ctypes.c_int]
+        lib.orc_gemm_naive_f32.argtypes = [P, P, P, I, I, I, I, I, I]
         _lib = lib
     return _lib
 
@@ -142,4 +143,15 @@ def gemm_bf16_f64(A, B, rows=None, nthreads: int = 1) -> np.ndarray:
     rows = np.arange(M, dtype=np.int64) if rows is None else np.ascontiguousarray(rows, dtype=np.int64)
     C = np.empty((rows.size, N), dtype=np.float64)
     _load().orc_gemm_bf16_f64(_p(A), _p(B), _p(C), M, N, K, _p(rows), rows.size, nthreads)
+    return C
+
+
+def gemm_naive_f32(A, B, M, N, K, lda, ldb, ldc) -> np.ndarray:
+    """C[M*ldc] fp32 per shaders/ops.metal:199-251 (sequential fp32 FMA chain
+    over k), A and B given as flat bf16 bit arrays with row strides lda / ldb."""
+    A = np.ascontiguousarray(A, dtype=np.uint16).ravel()
+    B = np.ascontiguousarray(B, dtype=np.uint16).ravel()
+    assert A.size >= (M - 1) * lda + K and B.size >= (N - 1) * ldb + K
+    C = np.zeros(M * ldc, dtype=np.float32)
+    _load().orc_gemm_naive_f32(_p(A), _p(B), _p(C), M, N, K, lda, ldb, ldc)
     return C

@@ -4,6 +4,7 @@
  * kernel-check loops (src/main.cpp:73-84 GEMV, src/main.cpp:594-601 GEMM).
  */
 #include "cpu_ref.h"
+#include <math.h>
 #include <string.h>
 
 float orc_bf16_to_f32(uint16_t v) {
@@ -148,4 +149,20 @@ void orc_gemm_bf16_f64(const uint16_t* A, const uint16_t* B, double* C,
             C[r * N + n] = acc;
         }
     }
+}
+
+void orc_gemm_naive_f32(const uint16_t* A, const uint16_t* B, float* C, int64_t M, int64_t N,
+                        int64_t K, int64_t lda, int64_t ldb, int64_t ldc) {
+    /* shaders/ops.metal:199-251 (gemm_naive): each output is one fp32 FMA
+     * chain acc = fma(A[m][k], B[n][k], acc) over k = 0..K-1 from +0, checked by
+     * src/main.cpp:578-602. A product of two bf16 values is exact in fp32, so
+     * the chain equals sequential multiply-then-add; the k order is the whole
+     * definition. */
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t n = 0; n < N; ++n) {
+            float acc = 0.0f;
+            for (int64_t k = 0; k < K; ++k)
+                acc = fmaf(orc_bf16_to_f32(A[m * lda + k]), orc_bf16_to_f32(B[n * ldb + k]), acc);
+            C[m * ldc + n] = acc;
+        }
 }

@@ -78,6 +78,11 @@ void orc_gemm_bf16_f64(const uint16_t* A, const uint16_t* B, double* C,
                        int64_t M, int64_t N, int64_t K, const int64_t* rows,
                        int64_t nrows, int nthreads);
 
+/* shaders/ops.metal:199-251 (gemm_naive), check src/main.cpp:578-602:
+ * C[m*ldc+n] = fp32 FMA chain over k = 0..K-1 of A[m*lda+k] * B[n*ldb+k]. */
+void orc_gemm_naive_f32(const uint16_t* A, const uint16_t* B, float* C, int64_t M, int64_t N,
+                        int64_t K, int64_t lda, int64_t ldb, int64_t ldc);
+
 #ifdef __cplusplus
 }
 #endif

@@ -65,6 +65,10 @@ def test_batched_and_gemm_argument_checks():
     assert _lib.status("miori_gemm_bf16", FAKE + 2, FAKE, FAKE, 16, 64, 128, 1, None) == -3
     assert _lib.status("miori_gemm_q4", FAKE, FAKE, FAKE, FAKE, FAKE, 16, 64, 128, 16, 0, None) == -2
     assert _lib.status("miori_dequant_q4", FAKE, FAKE, FAKE, FAKE, 64, 100, 64, None) == -2
+    assert _lib.status("miori_gemm_naive", 0, FAKE, FAKE, 4, 8, 32, 64, 32, 16, None) == -1
+    assert _lib.status("miori_gemm_naive", FAKE, FAKE, FAKE, 4, 8, 32, 16, 32, 16, None) == -2  # lda < K
+    assert _lib.status("miori_gemm_naive", FAKE, FAKE, FAKE, 4, 8, 32, 64, 32, 4, None) == -2   # ldc < N
+    assert _lib.status("miori_gemm_naive", FAKE + 1, FAKE, FAKE, 4, 8, 32, 64, 32, 16, None) == -3
     assert _lib.status("miori_dequant_q8", FAKE, FAKE, FAKE, 0, 64, 128, 64, None) == -1
 
 

@@ -196,3 +196,47 @@ def test_synth_distributions():
     # determinism
     np.testing.assert_array_equal(synth.quant_weights(8, 64, 32, 4, seed=9).q,
                                   synth.quant_weights(8, 64, 32, 4, seed=9).q)
+
+
+# ---- gemm_naive oracle (shaders/ops.metal:199-251; check src/main.cpp:578-602)
+
+def _bf(vals):
+    return synth.f32_to_bf16_bits(np.asarray(vals, dtype=np.float32))
+
+
+def test_naive_order_is_sequential_fp32():
+    """The definition is the k-ordered fp32 chain: 1 + 2^24 rounds back to 2^24
+    (tie to even), so [1, 2^24, -2^24] sums to 0 forwards while the exact
+    sum, and the reversed order, give 1. bf16 x bf16 products are exact in
+    fp32, so this pins the order and nothing else can differ."""
+    A = _bf([1.0, 4096.0, -4096.0])
+    B = _bf([1.0, 4096.0, 4096.0])
+    assert oracle.gemm_naive_f32(A, B, 1, 1, 3, 3, 3, 1)[0] == 0.0
+    assert oracle.gemm_naive_f32(A[::-1].copy(), B[::-1].copy(), 1, 1, 3, 3, 3, 1)[0] == 1.0
+
+
+def test_naive_integer_closed_form_with_strides():
+    """Small integers: every product and partial sum is exact, so the result
+    is the exact integer product. Strides, padding and the B^T orientation
+    are all pinned (a transposed operand or wrong stride changes the sums)."""
+    rng = np.random.default_rng(3)
+    M, N, K, lda, ldb, ldc = 5, 7, 40, 48, 43, 9
+    Ai = rng.integers(-8, 9, size=(M, lda))
+    Bi = rng.integers(-8, 9, size=(N, ldb))
+    C = oracle.gemm_naive_f32(_bf(Ai), _bf(Bi), M, N, K, lda, ldb, ldc).reshape(M, ldc)
+    exact = Ai[:, :K] @ Bi[:, :K].T
+    np.testing.assert_array_equal(C[:, :N], exact.astype(np.float32))
+    assert np.all(C[:, N:] == 0.0)  # outside the output columns nothing is written
+
+
+def test_naive_reference_case_vs_fp64():
+    """The reference's test-gemm inputs (src/main.cpp:578-602): M=4, N=8,
+    K=32, lda=64, ldb=32, ldc=16, a_i = bf16(sin(0.13 i)), b_i = bf16(cos(0.17 i));
+    the fp32 chain is within fp32 rounding of the fp64 product."""
+    M, N, K, lda, ldb, ldc = 4, 8, 32, 64, 32, 16
+    a = _bf(np.sin(np.arange(M * lda, dtype=np.float32) * np.float32(0.13)))
+    b = _bf(np.cos(np.arange(N * ldb, dtype=np.float32) * np.float32(0.17)))
+    C = oracle.gemm_naive_f32(a, b, M, N, K, lda, ldb, ldc).reshape(M, ldc)[:, :N]
+    af = synth.bf16_bits_to_f32(a).astype(np.float64).reshape(M, lda)[:, :K]
+    bf = synth.bf16_bits_to_f32(b).astype(np.float64).reshape(N, ldb)[:, :K]
+    np.testing.assert_allclose(C, af @ bf.T, rtol=0, atol=1e-5)
