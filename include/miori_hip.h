@@ -99,6 +99,24 @@ int miori_gemv_q8_batched(const void* q, const void* scales, const void* biases,
                           uint32_t K, uint32_t group, int out_dtype,
                           miori_stream stream);
 
+/* ---- fused decode ops ----------------------------------------------------
+ * The decode layer steps around the GEMVs, fused into the 4-bit GEMV so the
+ * bf16 activation never makes an HBM round trip (src/engine.cpp:388-400:
+ * rmsnorm -> gemv4 w1/w3, silu_mul -> gemv4 w2). One activation row.
+ *
+ * miori_rmsnorm_gemv_q4: y = W . h with h = bf16(x * rsqrt(sum(x^2)/K + eps) * w),
+ * x fp32 [K], w the bf16 norm weight [K] (rmsnorm, shaders/ops.metal:86-114).
+ * miori_silu_mul_gemv_q4: y = W . a with a = bf16(g / (1 + exp(-g)) * u), g and
+ * u fp32 [K] (silu_mul, shaders/ops.metal:129-139).
+ * Same shape/group/alignment rules as miori_gemv_q4, plus K <= 8192 and the
+ * fp32 / bf16 input vectors 16-byte aligned. */
+int miori_rmsnorm_gemv_q4(const float* x, const void* norm_weight, float eps, const void* q,
+                          const void* scales, const void* biases, void* y, uint32_t N,
+                          uint32_t K, uint32_t group, int out_dtype, miori_stream stream);
+int miori_silu_mul_gemv_q4(const float* gate, const float* up, const void* q,
+                           const void* scales, const void* biases, void* y, uint32_t N,
+                           uint32_t K, uint32_t group, int out_dtype, miori_stream stream);
+
 /* ---- prefill GEMMs ------------------------------------------------------
  * C[M][N] = A[M][K] . B[N][K]^T, bf16 operands, fp32 accumulation on MFMA.
  * B is the bf16 weight cache in this library's layout, which is plain

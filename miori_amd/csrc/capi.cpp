@@ -94,6 +94,30 @@ int miori_gemv_q4(const void* q, const void* scales, const void* biases, const v
                                        out_dtype == MIORI_BF16, (hipStream_t)stream));
 }
 
+int miori_rmsnorm_gemv_q4(const float* x, const void* norm_weight, float eps, const void* q,
+                          const void* scales, const void* biases, void* y, uint32_t N,
+                          uint32_t K, uint32_t group, int out_dtype, miori_stream stream) {
+    int st = check_gemv(4, q, scales, biases, x, y, 1, N, K, group, out_dtype);
+    if (st) return st;
+    if (!norm_weight) return MIORI_E_NULL;
+    if (K > 8192 || !(eps >= 0.f)) return MIORI_E_SHAPE;
+    if (!aligned(norm_weight, 16)) return MIORI_E_ALIGN;
+    return hip_status(launch_gemv_fused(1, q, scales, biases, x, norm_weight, eps, y, N, K, group,
+                                        out_dtype == MIORI_BF16, (hipStream_t)stream));
+}
+
+int miori_silu_mul_gemv_q4(const float* gate, const float* up, const void* q,
+                           const void* scales, const void* biases, void* y, uint32_t N,
+                           uint32_t K, uint32_t group, int out_dtype, miori_stream stream) {
+    int st = check_gemv(4, q, scales, biases, gate, y, 1, N, K, group, out_dtype);
+    if (st) return st;
+    if (!up) return MIORI_E_NULL;
+    if (K > 8192) return MIORI_E_SHAPE;
+    if (!aligned(up, 16)) return MIORI_E_ALIGN;
+    return hip_status(launch_gemv_fused(2, q, scales, biases, gate, up, 0.f, y, N, K, group,
+                                        out_dtype == MIORI_BF16, (hipStream_t)stream));
+}
+
 int miori_gemv_q8(const void* q, const void* scales, const void* biases, const void* x,
                   void* y, uint32_t N, uint32_t K, uint32_t group, int out_dtype,
                   miori_stream stream) {

@@ -76,11 +76,33 @@ __device__ __forceinline__ void prep_x(const u32x4_t (&d)[BITS == 4 ? 4 : 2], ui
     xs = sum;
 }
 
-template <int BITS, int MR, int R, int CPL>
+// Input transforms of the fused decode ops (one activation row, K <= 8192):
+// the bf16 x vector is built in LDS by the whole workgroup from fp32 inputs
+// that are L2-resident, so it never makes an HBM round trip.
+//   XM_NORM: x = bf16(xf * rsqrt(sum(xf^2)/K + eps) * w)     (ops.metal:86-114)
+//   XM_SILU: x = bf16(g / (1 + exp(-g)) * u)                 (ops.metal:129-139)
+enum { XM_PLAIN = 0, XM_NORM = 1, XM_SILU = 2 };
+constexpr uint32_t kXmMaxK = 8192;
+
+// bf16(silu(a) * u), silu(a) = a / (1 + e^-a), rounded as the CPU's expf
+// and IEEE divide would round it. The hardware exp2 of -a*log2(e) plus a
+// reciprocal is a few fp32 ulp off; that only matters when the fp32 product
+// lies near a bf16 rounding tie (low half 0x8000), where it can flip the
+// rounding. Those lanes (about 0.1%) recompute with expf and a divide.
+__device__ __forceinline__ uint32_t silu_mul_bf16(float a, float u) {
+    const float e = __builtin_amdgcn_exp2f(-a * 1.44269504088896341f);
+    float v = (a * __builtin_amdgcn_rcpf(1.0f + e)) * u;
+    const uint32_t lo = __builtin_bit_cast(uint32_t, v) & 0xFFFFu;
+    if (lo - (0x8000u - 32u) <= 64u) v = (a / (1.0f + expf(-a))) * u;
+    return f32_to_bf16_bits(v);
+}
+
+template <int BITS, int MR, int R, int CPL, int XM = XM_PLAIN>
 __global__ __launch_bounds__(256) void gemv_valu_kernel(
     const void* __restrict__ q, const void* __restrict__ s, const void* __restrict__ bs,
     const void* __restrict__ x, void* __restrict__ y, uint32_t N, uint32_t K, uint32_t G,
-    uint32_t S, int out_bf16) {
+    uint32_t S, int out_bf16, const void* __restrict__ x2 = nullptr, float eps = 0.f) {
+    static_assert(XM == XM_PLAIN || MR == 1, "fused input transforms take one row");
     constexpr uint32_t E = (BITS == 4) ? 32u : 16u;  // elements per 16-byte chunk
     constexpr int XL = (BITS == 4) ? 4 : 2;          // 16-byte x loads per chunk
     constexpr int RV0 = R * MR;
@@ -101,6 +123,31 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(
     const rsrc_t rs = make_rsrc(s, N * ng * 2u);
     const rsrc_t rb_ = make_rsrc(bs, N * ng * 2u);
     const rsrc_t rx = make_rsrc(x, MR * K * 2u);
+
+    // Fused transforms: issue the fp32 input loads before the weight loads
+    // (vmcnt completes in issue order, so waiting for them does not wait for
+    // the weight stream). Thread t owns elements 8t + 2048 i.
+    constexpr int XI = kXmMaxK / 2048;
+    __shared__ __attribute__((aligned(16))) uint16_t xl[XM == XM_PLAIN ? 8 : kXmMaxK];
+    f32x4_t xa[XM == XM_PLAIN ? 1 : XI][2], xb[XM == XM_PLAIN ? 1 : XI][2];
+    if constexpr (XM != XM_PLAIN) {
+        const rsrc_t r1 = make_rsrc(x, K * 4u);
+        const rsrc_t r2 = make_rsrc(x2, K * (XM == XM_NORM ? 2u : 4u));
+#pragma unroll
+        for (int i = 0; i < XI; ++i) {
+            const uint32_t e = i * 2048u + threadIdx.x * 8u;
+            const bool in = e < K;
+            xa[i][0] = __builtin_bit_cast(f32x4_t, buf_load16(r1, in ? e * 4u : kOOB));
+            xa[i][1] = __builtin_bit_cast(f32x4_t, buf_load16(r1, in ? e * 4u + 16u : kOOB));
+            if constexpr (XM == XM_NORM) {
+                const u32x4_t wv = buf_load16(r2, in ? e * 2u : kOOB);  // 8 bf16 weights
+                xb[i][0] = __builtin_bit_cast(f32x4_t, wv);
+            } else {
+                xb[i][0] = __builtin_bit_cast(f32x4_t, buf_load16(r2, in ? e * 4u : kOOB));
+                xb[i][1] = __builtin_bit_cast(f32x4_t, buf_load16(r2, in ? e * 4u + 16u : kOOB));
+            }
+        }
+    }
 
     uint32_t cidx[CPL];
     bool cval[CPL];
@@ -130,6 +177,50 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(
         }
     }
 
+    if constexpr (XM != XM_PLAIN) {
+        float inv = 0.f;
+        if constexpr (XM == XM_NORM) {
+            // sum of squares: per-thread, then the wave, then the 4 waves (fixed order)
+            float ss = 0.f;
+#pragma unroll
+            for (int i = 0; i < XI; ++i)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) ss = fmaf(xa[i][h][e], xa[i][h][e], ss);
+            ss = wave_sum(ss);
+            if (lane == 0) red[wave][0] = ss;
+            __syncthreads();
+            const float tot = ((red[0][0] + red[1][0]) + red[2][0]) + red[3][0];
+            inv = 1.0f / sqrtf(tot / (float)K + eps);
+        }
+#pragma unroll
+        for (int i = 0; i < XI; ++i) {
+            const uint32_t e = i * 2048u + threadIdx.x * 8u;
+            if (e >= K) continue;
+            uint32_t o[4];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                uint32_t v[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int j = 2 * p + h;  // element 8t + j
+                    const float a = xa[i][j >> 2][j & 3];
+                    if constexpr (XM == XM_NORM) {
+                        const uint32_t wb = __builtin_bit_cast(u32x4_t, xb[i][0])[j >> 1];
+                        v[h] = f32_to_bf16_bits((a * inv) *
+                                                bf16_bits_to_f32((wb >> (16 * (j & 1))) & 0xFFFFu));
+                    } else {
+                        v[h] = silu_mul_bf16(a, xb[i][j >> 2][j & 3]);
+                    }
+                }
+                o[p] = v[0] | (v[1] << 16);
+            }
+            *reinterpret_cast<u32x4_t*>(&xl[e]) = u32x4_t{o[0], o[1], o[2], o[3]};
+        }
+        __syncthreads();
+    }
+
     uint32_t xr[MR][CPL][16];
     float xs[MR][CPL];
 #pragma unroll
@@ -138,8 +229,14 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(
         for (int i = 0; i < CPL; ++i) {
             u32x4_t d[XL];
 #pragma unroll
-            for (int t = 0; t < XL; ++t)
-                d[t] = buf_load16(rx, cval[i] ? (m * K + cidx[i] * E) * 2u + t * 16u : kOOB);
+            for (int t = 0; t < XL; ++t) {
+                if constexpr (XM == XM_PLAIN) {
+                    d[t] = buf_load16(rx, cval[i] ? (m * K + cidx[i] * E) * 2u + t * 16u : kOOB);
+                } else {
+                    d[t] = cval[i] ? *reinterpret_cast<const u32x4_t*>(&xl[cidx[i] * E + t * 8u])
+                                   : u32x4_t{0u, 0u, 0u, 0u};
+                }
+            }
             prep_x<BITS>(d, xr[m][i], xs[m][i]);
         }
     }
@@ -208,6 +305,7 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(
                       (RV >= 4 || (RV == 2 ? (row16 & 1u) == 0u : row16 == 0u));
     const bool bf = out_bf16 != 0;
     if (S == 1) {
+        (void)x2;
         if (lead) {
 #pragma unroll
             for (int i = 0; i < (RV + 3) / 4; ++i) {
@@ -242,7 +340,7 @@ hipError_t launch_valu(const void* q, const void* s, const void* b, const void* 
     const uint32_t rows_per_wg = R * (4u / S);
     const uint32_t grid = (N + rows_per_wg - 1) / rows_per_wg;
     hipLaunchKernelGGL((gemv_valu_kernel<BITS, MR, R, CPL>), dim3(grid), dim3(256), 0, st,
-                       q, s, b, x, y, N, K, G, S, out_bf16);
+                       q, s, b, x, y, N, K, G, S, out_bf16, (const void*)nullptr, 0.f);
     return hipGetLastError();
 }
 
@@ -320,6 +418,49 @@ hipError_t launch_gemv_valu(int bits, const void* q, const void* s, const void* 
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+
+// Fused decode ops on the 4-bit GEMV, one activation row: y = W . t(x, x2)
+// with t = rmsnorm (xm = 1: x fp32, x2 bf16 norm weight, eps) or silu-mul
+// (xm = 2: x = gate fp32, x2 = up fp32). K <= 8192, a multiple of 32.
+hipError_t launch_gemv_fused(int xm, const void* q, const void* s, const void* b, const void* x,
+                             const void* x2, float eps, void* y, uint32_t N, uint32_t K,
+                             uint32_t G, int out_bf16, hipStream_t st) {
+    if (K > kXmMaxK || K % 32 != 0) return hipErrorInvalidValue;
+    uint32_t S;
+    int cpl;
+    gemv_split(4, K, &S, &cpl);
+    if (cpl != 1) return hipErrorInvalidValue;  // K <= 8192 takes one chunk per lane
+    // Every workgroup rebuilds the whole transformed vector, so that work
+    // grows with the grid: 8 rows per wave halve the grid once 4 rows would
+    // give 512 or more workgroups (N=8192 at K=2048, N=2048 at K=7680);
+    // smaller grids keep 4 rows so the weight stream has enough waves.
+    // MIORI_FUSED_ROWS=4|8 overrides the choice for tuning sweeps.
+    static const int r_env = [] {
+        const char* v = getenv("MIORI_FUSED_ROWS");
+        return v ? atoi(v) : 0;
+    }();
+    const int R = r_env == 8 || r_env == 4 ? r_env
+                  : (N + 4u * (4u / S) - 1) / (4u * (4u / S)) >= 512u ? 8 : 4;
+    const uint32_t rows_per_wg = R * (4u / S);
+    const dim3 grid((N + rows_per_wg - 1) / rows_per_wg);
+    if (xm != XM_NORM && xm != XM_SILU) return hipErrorInvalidValue;
+    if (R == 8) {
+        if (xm == XM_NORM)
+            hipLaunchKernelGGL((gemv_valu_kernel<4, 1, 8, 1, XM_NORM>), grid, dim3(256), 0, st, q,
+                               s, b, x, y, N, K, G, S, out_bf16, x2, eps);
+        else
+            hipLaunchKernelGGL((gemv_valu_kernel<4, 1, 8, 1, XM_SILU>), grid, dim3(256), 0, st, q,
+                               s, b, x, y, N, K, G, S, out_bf16, x2, eps);
+    } else {
+        if (xm == XM_NORM)
+            hipLaunchKernelGGL((gemv_valu_kernel<4, 1, 4, 1, XM_NORM>), grid, dim3(256), 0, st, q,
+                               s, b, x, y, N, K, G, S, out_bf16, x2, eps);
+        else
+            hipLaunchKernelGGL((gemv_valu_kernel<4, 1, 4, 1, XM_SILU>), grid, dim3(256), 0, st, q,
+                               s, b, x, y, N, K, G, S, out_bf16, x2, eps);
+    }
+    return hipGetLastError();
 }
 
 }  // namespace miori

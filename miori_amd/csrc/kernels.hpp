@@ -12,6 +12,11 @@ hipError_t launch_gemv_valu(int bits, const void* q, const void* s, const void* 
                             const void* x, void* y, uint32_t M, uint32_t N, uint32_t K,
                             uint32_t G, int out_bf16, hipStream_t st);
 void gemv_split(int bits, uint32_t K, uint32_t* S, int* cpl);
+// Fused decode ops on the 4-bit GEMV (one activation row, K <= 8192):
+// xm = 1: y = W . bf16(rmsnorm(x fp32) * w_norm bf16); xm = 2: y = W . bf16(silu(x) * x2)
+hipError_t launch_gemv_fused(int xm, const void* q, const void* s, const void* b, const void* x,
+                             const void* x2, float eps, void* y, uint32_t N, uint32_t K,
+                             uint32_t G, int out_bf16, hipStream_t st);
 
 
 // bf16 -> row-major bf16 dequant.

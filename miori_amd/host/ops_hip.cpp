@@ -112,6 +112,34 @@ void gemv4(Metal&, MTL::ComputeCommandEncoder* e, const Weights& w, const Tensor
     gemv_t(4, e, w, q, s, b, x, y, N, K, 1, 0, 0, false);
 }
 
+void rmsnorm_gemv4(Metal&, MTL::ComputeCommandEncoder* e, const Weights& w, const Tensor& q,
+                   const Tensor& s, const Tensor& b, MTL::Buffer* x, const Tensor& norm_w,
+                   MTL::Buffer* y, uint32_t N, uint32_t K, float eps) {
+    QArgs a = qargs(e, w, q, s, b, N, K, 4);
+    need_tensor(norm_w, (uint64_t)K * 2, "norm weight");
+    need(x, 0, (uint64_t)K * 4, "x");
+    need(y, 0, (uint64_t)N * 4, "y");
+    e->use_in(x);
+    e->use_out(y);
+    check(miori_rmsnorm_gemv_q4((const float*)x->gpu(), at(w.buffer(), norm_w.begin), eps, a.q,
+                                a.s, a.b, y->gpu(), N, K, a.G, MIORI_F32, e->stream()),
+          "rmsnorm_gemv4");
+}
+
+void silu_mul_gemv4(Metal&, MTL::ComputeCommandEncoder* e, const Weights& w, const Tensor& q,
+                    const Tensor& s, const Tensor& b, MTL::Buffer* gate, MTL::Buffer* up,
+                    MTL::Buffer* y, uint32_t N, uint32_t K) {
+    QArgs a = qargs(e, w, q, s, b, N, K, 4);
+    need(gate, 0, (uint64_t)K * 4, "gate");
+    need(up, 0, (uint64_t)K * 4, "up");
+    need(y, 0, (uint64_t)N * 4, "y");
+    e->use_in(gate); e->use_in(up);
+    e->use_out(y);
+    check(miori_silu_mul_gemv_q4((const float*)gate->gpu(), (const float*)up->gpu(), a.q, a.s,
+                                 a.b, y->gpu(), N, K, a.G, MIORI_F32, e->stream()),
+          "silu_mul_gemv4");
+}
+
 void gemv8(Metal&, MTL::ComputeCommandEncoder* e, const Weights& w, const Tensor& q,
            const Tensor& s, const Tensor& b, MTL::Buffer* x, MTL::Buffer* y, uint32_t N,
            uint32_t K) {

@@ -43,6 +43,16 @@ void dequant4(Metal& m, MTL::ComputeCommandEncoder* e, const Weights& w,
 void dequant_tile(Metal& m, MTL::ComputeCommandEncoder* e, const Weights& w,
                   const Tensor& q, const Tensor& s, const Tensor& b,
                   MTL::Buffer* out, uint32_t N, uint32_t K, uint32_t boff = 0);
+// Fused decode steps (no single reference function: the reference runs
+// rmsnorm then gemv4, and silu_mul then gemv4, src/engine.cpp:388-400).
+// norm_w is the bf16 norm weight tensor; x, gate and up are fp32 [K].
+void rmsnorm_gemv4(Metal& m, MTL::ComputeCommandEncoder* e, const Weights& w,
+                   const Tensor& q, const Tensor& s, const Tensor& b, MTL::Buffer* x,
+                   const Tensor& norm_w, MTL::Buffer* y, uint32_t N, uint32_t K,
+                   float eps = 1e-5f);
+void silu_mul_gemv4(Metal& m, MTL::ComputeCommandEncoder* e, const Weights& w,
+                    const Tensor& q, const Tensor& s, const Tensor& b, MTL::Buffer* gate,
+                    MTL::Buffer* up, MTL::Buffer* y, uint32_t N, uint32_t K);
 // src/ops.h:30-32 (fallback GEMM for any shape; fp32 C, strided operands)
 void gemm_naive(Metal& m, MTL::ComputeCommandEncoder* e, MTL::Buffer* A,
                 MTL::Buffer* B, MTL::Buffer* C, uint32_t M, uint32_t N, uint32_t K,

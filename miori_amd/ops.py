@@ -89,6 +89,34 @@ gemv4x4 = gemv4
 gemv4x2 = gemv4
 
 
+def rmsnorm_gemv4(x, norm_w, q, s, b, y, N, K, group=64, eps=1e-5, stream=None):
+    """Fused decode step y = W . bf16(rmsnorm(x) * norm_w): the reference's
+    rmsnorm -> gemv4 pair (src/engine.cpp:388-393; shaders/ops.metal:86-114,
+    6-42) in one launch. x fp32 [K], norm_w bf16 [K]."""
+    if K % group:
+        raise MioriError("miori_rmsnorm_gemv_q4", -2, "K must be a multiple of the group size")
+    if x.dtype != torch.float32 or norm_w.dtype not in (torch.bfloat16, torch.int16):
+        raise ValueError("x must be float32 and norm_w bf16")
+    qp, sp, bp = _qargs(q, s, b, N, K, group, 4)
+    _lib.call("miori_rmsnorm_gemv_q4", _ptr(x, "x", K * 4), _ptr(norm_w, "norm_w", K * 2),
+              float(eps), qp, sp, bp, _ptr(y, "y", N * y.element_size()), N, K, group,
+              _out_dtype(y), _stream(stream))
+
+
+def silu_mul_gemv4(gate, up, q, s, b, y, N, K, group=64, stream=None):
+    """Fused decode step y = W . bf16(silu(gate) * up): the reference's
+    silu_mul -> gemv4 w2 pair (src/engine.cpp:396-398; shaders/ops.metal:129-139,
+    6-42) in one launch. gate, up fp32 [K]."""
+    if K % group:
+        raise MioriError("miori_silu_mul_gemv_q4", -2, "K must be a multiple of the group size")
+    if gate.dtype != torch.float32 or up.dtype != torch.float32:
+        raise ValueError("gate and up must be float32")
+    qp, sp, bp = _qargs(q, s, b, N, K, group, 4)
+    _lib.call("miori_silu_mul_gemv_q4", _ptr(gate, "gate", K * 4), _ptr(up, "up", K * 4),
+              qp, sp, bp, _ptr(y, "y", N * y.element_size()), N, K, group, _out_dtype(y),
+              _stream(stream))
+
+
 def gemv8(q, s, b, x, y, N, K, group=64, stream=None):
     """8-bit lm_head GEMV (src/ops.h:12-14; kernel shaders/ops.metal:46-82)."""
     _gemv("miori_gemv_q8", 8, q, s, b, x, y, N, K, 1, group, stream)

@@ -54,6 +54,8 @@ def _load():
             getattr(lib, name).argtypes = [P, P, P, P, P, I, I, I, I, I, I, ctypes.c_int]
         lib.orc_gemm_bf16_f64.argtypes = [P, P, P, I, I, I, P, I, ctypes.c_int]
         lib.orc_gemm_naive_f32.argtypes = [P, P, P, I, I, I, I, I, I]
+        lib.orc_rmsnorm_bf16.argtypes = [P, P, P, I, ctypes.c_float]
+        lib.orc_silu_mul_bf16.argtypes = [P, P, P, I]
         _lib = lib
     return _lib
 
@@ -155,3 +157,21 @@ def gemm_naive_f32(A, B, M, N, K, lda, ldb, ldc) -> np.ndarray:
     C = np.zeros(M * ldc, dtype=np.float32)
     _load().orc_gemm_naive_f32(_p(A), _p(B), _p(C), M, N, K, lda, ldb, ldc)
     return C
+
+
+def rmsnorm_bf16(x, w, eps: float) -> np.ndarray:
+    """bf16 bits of rmsnorm(x) * w per shaders/ops.metal:86-114 (one row)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.uint16)
+    h = np.empty(x.size, dtype=np.uint16)
+    _load().orc_rmsnorm_bf16(_p(x), _p(w), _p(h), x.size, eps)
+    return h
+
+
+def silu_mul_bf16(g, u) -> np.ndarray:
+    """bf16 bits of silu(g) * u per shaders/ops.metal:129-139."""
+    g = np.ascontiguousarray(g, dtype=np.float32)
+    u = np.ascontiguousarray(u, dtype=np.float32)
+    a = np.empty(g.size, dtype=np.uint16)
+    _load().orc_silu_mul_bf16(_p(g), _p(u), _p(a), g.size)
+    return a

@@ -166,3 +166,18 @@ void orc_gemm_naive_f32(const uint16_t* A, const uint16_t* B, float* C, int64_t 
             C[m * ldc + n] = acc;
         }
 }
+
+void orc_rmsnorm_bf16(const float* x, const uint16_t* w, uint16_t* h, int64_t K, float eps) {
+    /* shaders/ops.metal:86-114 (rmsnorm, one row): inv = rsqrt(sum(x^2)/n + eps),
+     * y = bfloat(x * inv * float(w)). The sum runs in k order here; the GPU
+     * sums in another fixed order, which moves inv by at most a few ulp. */
+    float ss = 0.0f;
+    for (int64_t k = 0; k < K; ++k) ss = fmaf(x[k], x[k], ss);
+    const float inv = 1.0f / sqrtf(ss / (float)K + eps);
+    for (int64_t k = 0; k < K; ++k) h[k] = orc_f32_to_bf16((x[k] * inv) * orc_bf16_to_f32(w[k]));
+}
+
+void orc_silu_mul_bf16(const float* g, const float* u, uint16_t* a, int64_t K) {
+    /* shaders/ops.metal:129-139 (silu_mul): out = bfloat(g / (1 + exp(-g)) * up). */
+    for (int64_t k = 0; k < K; ++k) a[k] = orc_f32_to_bf16((g[k] / (1.0f + expf(-g[k]))) * u[k]);
+}

@@ -83,6 +83,11 @@ void orc_gemm_bf16_f64(const uint16_t* A, const uint16_t* B, double* C,
 void orc_gemm_naive_f32(const uint16_t* A, const uint16_t* B, float* C, int64_t M, int64_t N,
                         int64_t K, int64_t lda, int64_t ldb, int64_t ldc);
 
+/* shaders/ops.metal:86-114: h = bf16(x * rsqrt(sum(x^2)/K + eps) * w), one row. */
+void orc_rmsnorm_bf16(const float* x, const uint16_t* w, uint16_t* h, int64_t K, float eps);
+/* shaders/ops.metal:129-139: a = bf16(g / (1 + exp(-g)) * u). */
+void orc_silu_mul_bf16(const float* g, const float* u, uint16_t* a, int64_t K);
+
 #ifdef __cplusplus
 }
 #endif

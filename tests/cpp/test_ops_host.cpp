@@ -115,6 +115,15 @@ int main(int argc, char** argv) {
     std::vector<Entry> es;
     quant("layers.2.self_attn.q_proj", 4, N, K, G, es);
     quant("embed_tokens", 8, NV, K, G, es);
+    {
+        Entry nw{"layers.2.input_layernorm.weight", "BF16", {K}, {}};
+        nw.bytes.resize((size_t)K * 2);
+        for (int64_t k = 0; k < K; ++k) {
+            const uint16_t v = orc_f32_to_bf16((float)(0.8 + 0.4 * uni()));
+            memcpy(&nw.bytes[2 * k], &v, 2);
+        }
+        es.push_back(std::move(nw));
+    }
     write_safetensors(path, es);
 
     Metal m;
@@ -123,7 +132,7 @@ int main(int argc, char** argv) {
     m.print_info();
     Weights w;
     if (!w.load(m, path, err)) { printf("FAIL load: %s\n", err.c_str()); return 2; }
-    expect(w.tensor_count() == 6, "safetensors loader: 6 tensors");
+    expect(w.tensor_count() == 7, "safetensors loader: 7 tensors");
     const Tensor& q = w.get("layers.2.self_attn.q_proj.weight");
     const Tensor& s = w.get("layers.2.self_attn.q_proj.scales");
     const Tensor& b = w.get("layers.2.self_attn.q_proj.biases");
@@ -220,6 +229,72 @@ int main(int argc, char** argv) {
         const float* c2 = (const float*)C2->contents();
         expect(close_enough(c1, cref.data(), (size_t)M * N, "gemm_mpp"), "gemm_mpp vs oracle");
         expect(memcmp(c1, c2, (size_t)M * N * 4) == 0, "gemm_q4 bit-identical to dequant_tile + gemm_mpp");
+    }
+
+    // ---- fused decode steps: rmsnorm -> gemv4 and silu_mul -> gemv4
+    {
+        const Tensor& nw = w.get("layers.2.input_layernorm.weight");
+        MTL::Buffer* xf = m.new_buffer((size_t)K * 4);
+        MTL::Buffer* uf = m.new_buffer((size_t)K * 4);
+        float* xfp = (float*)xf->contents();
+        float* ufp = (float*)uf->contents();
+        for (int64_t k = 0; k < K; ++k) {
+            xfp[k] = (float)(3.0 * (uni() - 0.5));
+            ufp[k] = (float)(2.0 * (uni() - 0.5));
+        }
+        auto cb = m.begin();
+        auto e = cb->computeCommandEncoder();
+        rmsnorm_gemv4(m, e, w, q, s, b, xf, nw, y, (uint32_t)N, (uint32_t)K, 1e-5f);
+        m.submit(cb, true);
+        std::vector<uint16_t> h((size_t)K);
+        xfp = (float*)xf->contents();
+        orc_rmsnorm_bf16(xfp, (const uint16_t*)nw.ptr, h.data(), K, 1e-5f);
+        orc_gemv4_f64((const uint32_t*)q.ptr, (const uint16_t*)s.ptr, (const uint16_t*)b.ptr,
+                      h.data(), ref.data(), 1, N, K, G, 8);
+        expect(close_enough((const float*)y->contents(), ref.data(), N, "rmsnorm_gemv4"),
+               "rmsnorm_gemv4 vs oracle");
+        cb = m.begin();
+        e = cb->computeCommandEncoder();
+        silu_mul_gemv4(m, e, w, q, s, b, xf, uf, y, (uint32_t)N, (uint32_t)K);
+        m.submit(cb, true);
+        xfp = (float*)xf->contents();
+        ufp = (float*)uf->contents();
+        orc_silu_mul_bf16(xfp, ufp, h.data(), K);
+        orc_gemv4_f64((const uint32_t*)q.ptr, (const uint16_t*)s.ptr, (const uint16_t*)b.ptr,
+                      h.data(), ref.data(), 1, N, K, G, 8);
+        expect(close_enough((const float*)y->contents(), ref.data(), N, "silu_mul_gemv4"),
+               "silu_mul_gemv4 vs oracle");
+        xf->release(); delete xf;
+        uf->release(); delete uf;
+    }
+
+    // ---- gemm_naive: the reference's test-gemm case (src/main.cpp:578-602),
+    // M=4 N=8 K=32 with lda=64 ldb=32 ldc=16, bit-exact against the
+    // sequential fp32 FMA chain
+    {
+        const uint32_t M = 4, NN = 8, KK = 32, lda = 64, ldb = 32, ldc = 16;
+        MTL::Buffer* A = m.new_buffer((size_t)M * lda * 2);
+        MTL::Buffer* Bm = m.new_buffer((size_t)NN * ldb * 2);
+        MTL::Buffer* C = m.new_buffer((size_t)M * ldc * 4);
+        uint16_t* ap = (uint16_t*)A->contents();
+        uint16_t* bp = (uint16_t*)Bm->contents();
+        for (uint32_t i = 0; i < M * lda; ++i) ap[i] = orc_f32_to_bf16((float)(2.0 * uni() - 1.0));
+        for (uint32_t i = 0; i < NN * ldb; ++i) bp[i] = orc_f32_to_bf16((float)(2.0 * uni() - 1.0));
+        float* cp = (float*)C->contents();
+        for (uint32_t i = 0; i < M * ldc; ++i) cp[i] = -7.f;   // untouched padding columns
+        auto cb = m.begin();
+        auto e = cb->computeCommandEncoder();
+        gemm_naive(m, e, A, Bm, C, M, NN, KK, lda, ldb, ldc);
+        m.submit(cb, true);
+        std::vector<float> cref((size_t)M * ldc, -7.f);
+        ap = (uint16_t*)A->contents();
+        bp = (uint16_t*)Bm->contents();
+        orc_gemm_naive_f32(ap, bp, cref.data(), M, NN, KK, lda, ldb, ldc);
+        expect(memcmp(C->contents(), cref.data(), cref.size() * 4) == 0,
+               "gemm_naive bit-exact vs sequential fp32 chain (padding untouched)");
+        A->release(); delete A;
+        Bm->release(); delete Bm;
+        C->release(); delete C;
     }
 
     // ---- errors surface as exceptions, as the reference's Metal::pso does

@@ -240,3 +240,48 @@ def test_naive_reference_case_vs_fp64():
     af = synth.bf16_bits_to_f32(a).astype(np.float64).reshape(M, lda)[:, :K]
     bf = synth.bf16_bits_to_f32(b).astype(np.float64).reshape(N, ldb)[:, :K]
     np.testing.assert_allclose(C, af @ bf.T, rtol=0, atol=1e-5)
+
+
+# ---- fused decode-op transforms (shaders/ops.metal:86-114 rmsnorm, :129-139 silu_mul)
+
+def _bf_ulp_diff(a_bits, b_bits):
+    a = a_bits.astype(np.int32)
+    b = b_bits.astype(np.int32)
+    return np.abs(a - b)
+
+
+def test_rmsnorm_closed_form():
+    """x = 2 everywhere: sum(x^2)/K = 4 exactly, rsqrt(4 + 0) = 0.5 exactly, so
+    h = bf16(1 * w) = w bit for bit. A sum instead of a mean, or a missing
+    square, breaks it."""
+    K = 2048
+    w = synth.activations(1, K, seed=5).ravel()
+    h = oracle.rmsnorm_bf16(np.full(K, 2.0, np.float32), w, 0.0)
+    np.testing.assert_array_equal(h, w)
+
+
+def test_rmsnorm_vs_torch_fp64():
+    K = 2048
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal(K) * 3).astype(np.float32)
+    w = _bf(rng.standard_normal(K) * 0.2 + 1.0)
+    h = oracle.rmsnorm_bf16(x, w, 1e-5)
+    xt = torch.tensor(x, dtype=torch.float64)
+    ref = xt / torch.sqrt((xt * xt).mean() + 1e-5) * torch.tensor(synth.bf16_bits_to_f32(w), dtype=torch.float64)
+    ref_bits = synth.f32_to_bf16_bits(ref.float().numpy())
+    d = _bf_ulp_diff(h, ref_bits)
+    assert d.max() <= 1 and (d == 0).mean() > 0.98
+
+
+def test_silu_mul_vs_torch_fp64_and_limits():
+    rng = np.random.default_rng(2)
+    g = (rng.standard_normal(4096) * 4).astype(np.float32)
+    u = (rng.standard_normal(4096)).astype(np.float32)
+    a = oracle.silu_mul_bf16(g, u)
+    ref = torch.nn.functional.silu(torch.tensor(g, dtype=torch.float64)) * torch.tensor(u, dtype=torch.float64)
+    d = _bf_ulp_diff(a, synth.f32_to_bf16_bits(ref.float().numpy()))
+    assert d.max() <= 1 and (d == 0).mean() > 0.98
+    # silu(0) = 0, silu(g) -> g for large g, silu(-g) -> 0 for large g
+    lim = oracle.silu_mul_bf16(np.array([0.0, 40.0, -40.0], np.float32), np.ones(3, np.float32))
+    v = synth.bf16_bits_to_f32(lim)
+    assert v[0] == 0.0 and v[1] == 40.0 and abs(v[2]) < 1e-15
