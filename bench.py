@@ -218,6 +218,55 @@ def chain_case(torch, ops, synth, dev, M, timer, layers=24, G=64, steps=3, warmu
     return res
 
 
+def fused_decode_case(torch, ops, synth, dev, N, K, timer, steps, warmup, G=64):
+    """Fused decode steps (rmsnorm -> gemv4 and silu_mul -> gemv4, as the
+    reference's engine.cpp:388-400 runs them in two launches) against the
+    plain gemv4 on the same rotating weights: the fused launch reads the fp32
+    input (and the bf16 norm weight) instead of a bf16 activation."""
+    w = synth.quant_weights(N, K, G, 4, seed=synth.BASE_SEED + 7 * N + K)
+    base = ops.QuantLinear(w, dev)
+    copies = max(1, math.ceil(ROTATE_BYTES / w.nbytes))
+    qs = [base.q] + [base.q.clone() for _ in range(copies - 1)]
+    ss = [base.s] + [base.s.clone() for _ in range(copies - 1)]
+    bs = [base.b] + [base.b.clone() for _ in range(copies - 1)]
+    xb = ops.to_device_bits(synth.activations(1, K), dev)
+    xf = torch.randn(K, device=dev)
+    up = torch.randn(K, device=dev)
+    nw = (torch.rand(K, device=dev) + 0.5).to(torch.bfloat16)
+    y = torch.empty(N, dtype=torch.bfloat16, device=dev)
+    res = dict(N=N, K=K, G=G, copies=copies)
+    cases = {
+        "gemv4": (lambda j: ops.gemv4(qs[j], ss[j], bs[j], xb, y, N, K, group=G), K * 2),
+        "rmsnorm_gemv4": (lambda j: ops.rmsnorm_gemv4(xf, nw, qs[j], ss[j], bs[j], y, N, K,
+                                                      group=G), K * 6),
+        "silu_mul_gemv4": (lambda j: ops.silu_mul_gemv4(xf, up, qs[j], ss[j], bs[j], y, N, K,
+                                                        group=G), K * 8),
+    }
+    for name, (f, xbytes) in cases.items():
+        total, mode = timer.run(lambda i: f(i % copies), steps, warmup)
+        per = total / steps
+        res[name + "_us"] = per * 1e3
+        res[name + "_gbs"] = (w.nbytes + xbytes + N * 2) / (per * 1e-3) / 1e9
+    res["mode"] = mode
+    del qs, ss, bs, base
+    torch.cuda.empty_cache()
+    return res
+
+
+def naive_case(torch, ops, dev, M, N, K, timer, steps, warmup):
+    """gemm_naive, the any-shape fallback: C fp32 [M][N] = A [M][K] . B [N][K]^T,
+    bf16 operands (the N=16 gate_proj and the bf16 batch lm_head)."""
+    A = torch.randn(M, K, device=dev).to(torch.bfloat16)
+    B = torch.randn(N, K, device=dev).to(torch.bfloat16)
+    C = torch.empty(M, N, dtype=torch.float32, device=dev)
+    total, mode = timer.run(lambda i: ops.gemm_naive(A, B, C, M, N, K, K, K, N), steps, warmup)
+    per = total / steps
+    algo = (M * K + N * K) * 2 + M * N * 4
+    return dict(M=M, N=N, K=K, mode=mode, us_kernel=per * 1e3,
+                gbs_kernel=algo / (per * 1e-3) / 1e9,
+                tflops_kernel=2.0 * M * N * K / (per * 1e-3) / 1e12)
+
+
 def calib_copy(torch, dev):
     """A plain 256 MiB device copy: reads and writes exactly 256 MiB, the
     reference for scaling FETCH_SIZE / WRITE_SIZE counters to bytes."""
@@ -339,6 +388,13 @@ def run_all(torch, ops, synth, oracle, dev, timer):
                                  **gemm_case(torch, ops, synth, oracle, dev, M, N, K, fused,
                                              timer, 30, 3)))
                 print(f"[bench] {rows[-1]}", file=sys.stderr, flush=True)
+    for (K, N) in [(2048, 2048), (2048, 8192), (7680, 2048), (8192, 2048)]:
+        rows.append(dict(row="fused-decode", **fused_decode_case(torch, ops, synth, dev, N, K,
+                                                                timer, st, wu)))
+        print(f"[bench] {rows[-1]}", file=sys.stderr, flush=True)
+    for (M, N, K) in [(1, 16, 2048), (32, 16, 2048), (8, 131072, 2048), (32, 131072, 2048)]:
+        rows.append(dict(row="gemm_naive", **naive_case(torch, ops, dev, M, N, K, timer, 20, 3)))
+        print(f"[bench] {rows[-1]}", file=sys.stderr, flush=True)
     return rows
 
 
