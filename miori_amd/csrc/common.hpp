@@ -77,6 +77,15 @@ constexpr uint32_t kOOB = 0xFFFFFFF0u;  // an offset that is always out of range
 __device__ __forceinline__ u32x4_t buf_load16(rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
 }
+// AUX: cache-policy bits of the load (2 = nt, streaming data read once)
+template <int AUX>
+__device__ __forceinline__ u32x4_t buf_load16_aux(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, AUX);
+}
+template <int AUX>
+__device__ __forceinline__ uint32_t buf_load_u16_aux(rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, AUX);
+}
 __device__ __forceinline__ uint32_t buf_load_u16(rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
 }

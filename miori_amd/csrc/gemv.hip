@@ -158,8 +158,29 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(
         cidx[i] = c;
     }
 
-    // Weight loads for all R rows first: they are the HBM stream. Rows past
-    // N and chunks past the row read as zero (out-of-range buffer offsets).
+    // x chunks (plain GEMV) are loaded before the weights: they come from L2
+    // and, since vmcnt completes in issue order, loading them after the
+    // weights would hold the x preparation (and every row's arithmetic) until
+    // the last weight byte has landed. Issued first, they are ready while the
+    // weight stream is still in flight, and row r's arithmetic waits only for
+    // the loads of rows 0..r.
+    u32x4_t xd[XM == XM_PLAIN ? MR : 1][CPL][XL];
+    if constexpr (XM == XM_PLAIN) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m)
+#pragma unroll
+            for (int i = 0; i < CPL; ++i)
+#pragma unroll
+                for (int t = 0; t < XL; ++t)
+                    xd[m][i][t] = buf_load16(rx, cval[i] ? (m * K + cidx[i] * E) * 2u + t * 16u : kOOB);
+    }
+
+    // Weight loads for all R rows, row by row: they are the HBM stream. Rows
+    // past N and chunks past the row read as zero (out-of-range offsets).
+    // Weights are read once per launch, so their loads are non-temporal (nt);
+    // so are the 4-bit scales/biases (measured faster), while the 8-bit
+    // lm_head keeps its scales/biases cached (measured faster that way).
+    constexpr int kQAux = 2, kSbAux = BITS == 4 ? 2 : 0;
     u32x4_t qv[R][CPL];
     uint32_t sv[R][CPL], bv[R][CPL];
 #pragma unroll
@@ -169,11 +190,11 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
             const bool ok = rv && cval[i];
-            qv[r][i] = buf_load16(rq, ok ? (row * C + cidx[i]) * 16u : kOOB);
+            qv[r][i] = buf_load16_aux<kQAux>(rq, ok ? (row * C + cidx[i]) * 16u : kOOB);
             const uint32_t g = cidx[i] * E / G;
             const uint32_t so = ok ? (row * ng + g) * 2u : kOOB;
-            sv[r][i] = buf_load_u16(rs, so);
-            bv[r][i] = buf_load_u16(rb_, so);
+            sv[r][i] = buf_load_u16_aux<kSbAux>(rs, so);
+            bv[r][i] = buf_load_u16_aux<kSbAux>(rb_, so);
         }
     }
 
@@ -231,7 +252,7 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(
 #pragma unroll
             for (int t = 0; t < XL; ++t) {
                 if constexpr (XM == XM_PLAIN) {
-                    d[t] = buf_load16(rx, cval[i] ? (m * K + cidx[i] * E) * 2u + t * 16u : kOOB);
+                    d[t] = xd[m][i][t];
                 } else {
                     d[t] = cval[i] ? *reinterpret_cast<const u32x4_t*>(&xl[cidx[i] * E + t * 8u])
                                    : u32x4_t{0u, 0u, 0u, 0u};
