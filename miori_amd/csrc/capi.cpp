@@ -59,6 +59,8 @@ int check_gemm(const void* A, const void* C, uint32_t M, uint32_t N, uint32_t K,
     if (!A || !C) return MIORI_E_NULL;
     if (out_dtype != MIORI_F32 && out_dtype != MIORI_BF16) return MIORI_E_DTYPE;
     if (M == 0 || N == 0 || K == 0 || K % 64 != 0 || N % 16 != 0) return MIORI_E_SHAPE;
+    // The GEMM addresses A and B rows with 32-bit byte offsets.
+    if ((uint64_t)M * K * 2 > kMaxBytes || (uint64_t)N * K * 2 > kMaxBytes) return MIORI_E_SHAPE;
     if (!aligned(A, 16) || !aligned(C, 16)) return MIORI_E_ALIGN;
     return MIORI_OK;
 }

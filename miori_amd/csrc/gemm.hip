@@ -155,20 +155,31 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     };
 
     // bf16 path: DMA instruction p (0 <= p < L) of group kt into stage st, so
-    // a group can be spread over the MFMA stream.
+    // a group can be spread over the MFMA stream. Issued between MFMAs, so it
+    // must cost no vector instructions: the per-lane byte offsets (row and
+    // swizzled chunk) are computed once, the K-slice base is a wave-uniform
+    // pointer (global_load_lds with an SGPR base and a VGPR offset), and the
+    // LDS destination comes from the wave index held in an SGPR, so M0 is set
+    // by scalar instructions.
+    const uint32_t wave_s = __builtin_amdgcn_readfirstlane(wave);
+    uint32_t ab_off[Q4 ? 1 : CF::L];
+    if constexpr (!Q4) {
+#pragma unroll
+        for (int p = 0; p < CF::L; ++p) {
+            const bool is_a = p < CF::A_INS;
+            const int pp = is_a ? p : p - CF::A_INS;
+            const uint32_t r = (wave * (is_a ? CF::A_INS : CF::B_INS) + pp) * 8u + (lane >> 3);
+            const uint32_t kb = (lane & 7u) ^ (r & 7u) ^ ((r >> 3) & 1u);
+            const uint32_t row = is_a ? min(m0 + r, M - 1u) : min(n0 + r, N - 1u);
+            ab_off[p] = row * K * 2u + kb * 16u;
+        }
+    }
     auto issue_one = [&](uint32_t kt, uint32_t st, int p) {
         const bool is_a = p < CF::A_INS;
         const int pp = is_a ? p : p - CF::A_INS;
-        const uint32_t r0 = (wave * (is_a ? CF::A_INS : CF::B_INS) + pp) * 8u;
-        const uint32_t r = r0 + (lane >> 3);
-        const uint32_t kb = (lane & 7u) ^ (r & 7u) ^ ((r >> 3) & 1u);
-        if (is_a) {
-            const uint32_t row = min(m0 + r, M - 1u);
-            dma16(A + (size_t)row * K + (kt0 + kt) * BK + kb * 8u, lds + CF::A_OFF + st * CF::A_ST + r0 * ROWB);
-        } else {
-            const uint32_t row = min(n0 + r, N - 1u);
-            dma16(B + (size_t)row * K + (kt0 + kt) * BK + kb * 8u, lds + CF::B_OFF + st * CF::B_ST + r0 * ROWB);
-        }
+        const uint32_t r0 = (wave_s * (is_a ? CF::A_INS : CF::B_INS) + pp) * 8u;
+        const uint8_t* base = reinterpret_cast<const uint8_t*>(is_a ? A : B) + (size_t)(kt0 + kt) * BK * 2u;
+        dma16(base + ab_off[p], lds + (is_a ? CF::A_OFF + st * CF::A_ST : CF::B_OFF + st * CF::B_ST) + r0 * ROWB);
     };
 
     // Fused 4-bit: dequantise raw slot `stage` into bf16 buffer bb.
@@ -346,6 +357,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(
             __builtin_amdgcn_sched_barrier(0);
         }
     }
+
+    // Every fragment read has landed before any epilogue code runs: the last
+    // k-step already waited for them, but the epilogue's address arithmetic
+    // must not be scheduled above a point where that holds on every path.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 
     // Epilogue through LDS (the stage buffers are free once every wave is past
     // the loop). Accumulator element e of lane l is row 8*(e/4) + 4*(l/32) +

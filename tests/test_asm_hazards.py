@@ -1,6 +1,8 @@
-"""The skinny kernel's hand-placed vmcnt waits, checked on its gfx950
-assembly: no register of a pending load is read or reused early (such a read
-gives wrong values; a reuse as an address faults the GPU)."""
+"""Hand-placed load waits, checked on the gfx950 assembly of the kernels that
+use them (the skinny kernel's inline-asm buffer loads under vmcnt, the GEMM's
+inline-asm LDS fragment reads under lgkmcnt): no register of a pending load
+is read or reused early on any control-flow path (such a read gives wrong
+values; a reuse as an address faults the GPU)."""
 import os
 import re
 import shutil
@@ -24,6 +26,56 @@ def test_checker_catches_early_use():
     lines = [(1, "global_load_dword v2, v[0:1], off"), (2, "global_load_dword v3, v[0:1], off"),
              (3, "s_waitcnt vmcnt(1)"), (4, "v_add_u32_e32 v4, v2, v2"), (5, "v_add_u32_e32 v5, v3, v3")]
     assert [b[0] for b in check_kernel(lines)] == [5]
+
+
+def test_checker_follows_control_flow():
+    # an LDS read issued before a loop is still pending in the loop body
+    lines = [(1, "ds_read_b128 v[2:5], v0"), (2, ".LBB0_1:"), (3, "v_add_u32_e32 v7, v2, v2"),
+             (4, "s_waitcnt lgkmcnt(0)"), (5, "s_cbranch_scc1 .LBB0_1"), (6, "s_endpgm")]
+    assert [b[0] for b in check_kernel(lines)] == [3]
+    # a read issued at the bottom of the loop reaches the top over the back edge
+    lines = [(1, ".LBB0_1:"), (2, "v_mov_b32_e32 v3, 0"), (3, "ds_read_b32 v3, v0"),
+             (4, "s_cbranch_scc1 .LBB0_1"), (5, "s_waitcnt lgkmcnt(0)"), (6, "s_endpgm")]
+    assert [b[0] for b in check_kernel(lines)] == [2]
+    # the compiler's if/else flag idiom: only the path that waited branches
+    # to the consumer, so no violation
+    lines = [(1, "ds_read_b128 v[2:5], v0"), (2, "s_mov_b64 s[4:5], -1"),
+             (3, "s_cbranch_scc0 .LBB0_2"), (4, "s_waitcnt lgkmcnt(0)"), (5, "s_mov_b64 s[4:5], 0"),
+             (6, ".LBB0_2:"), (7, "s_andn2_b64 vcc, exec, s[4:5]"), (8, "s_cbranch_vccnz .LBB0_3"),
+             (9, "s_endpgm"), (10, ".LBB0_3:"), (11, "v_mfma_f32_32x32x16_bf16 a[0:15], v[2:5], v[2:5], a[0:15]"),
+             (12, "s_endpgm")]
+    assert check_kernel(lines) == []
+    # the same without the wait on the branching path is caught
+    lines[3] = (4, "s_nop 0")
+    assert [b[0] for b in check_kernel(lines)] == [11]
+    # a pending LDS read whose destination is reused by arithmetic (the
+    # compiler does this when the read's result is dead)
+    lines = [(1, "ds_read_b128 v[6:9], v0"), (2, "v_add_u32_e32 v6, 16, v16"),
+             (3, "global_load_lds_dwordx4 v[6:7], off"), (4, "s_endpgm")]
+    assert [b[0] for b in check_kernel(lines)] == [2, 3]
+
+
+def _compile(src, out):
+    cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",
+           "-Xclang", "-packed-fp32-ops", "--cuda-device-only", "-S", "-I", CSRC,
+           "-o", str(out), os.path.join(CSRC, src)]
+    subprocess.run(cmd, check=True, capture_output=True, timeout=600)
+    return out.read_text()
+
+
+def _spilled(text, name):
+    scratch = re.findall(r"\.name:\s+(\S+)(?:(?!\.name:).)*?\.private_segment_fixed_size:\s+(\d+)", text, re.S)
+    return [n for n, sz in scratch if name in n and int(sz) > 0]
+
+
+@pytest.mark.skipif(not shutil.which(HIPCC) and not os.path.exists(HIPCC), reason="hipcc not available")
+def test_gemm_kernel_waits(tmp_path):
+    text = _compile("gemm.hip", tmp_path / "gemm.s")
+    res = check_file(text, "gemm_kernel")
+    assert len(res) == 8, "expected every gemm_kernel instantiation"
+    bad = {k: v for k, v in res.items() if v}
+    assert not bad, {k[:80]: v[:3] for k, v in bad.items()}
+    assert not _spilled(text, "gemm_kernel")
 
 
 @pytest.mark.skipif(not shutil.which(HIPCC) and not os.path.exists(HIPCC), reason="hipcc not available")
