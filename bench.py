@@ -142,7 +142,8 @@ def gemv_case(torch, ops, synth, dev, bits, M, N, K, G, out_dtype, timer, steps,
     return res
 
 
-def gemm_case(torch, ops, synth, oracle_mod, dev, M, N, K, fused, timer, steps, warmup, G=64):
+def gemm_case(torch, ops, synth, oracle_mod, dev, M, N, K, fused, timer, steps, warmup, G=64,
+              vendor=False):
     w = synth.quant_weights(N, K, G, 4, seed=synth.BASE_SEED + N + K)
     lin = ops.QuantLinear(w, dev)
     A = ops.to_device_bits(synth.activations(M, K), dev)
@@ -171,12 +172,20 @@ def gemm_case(torch, ops, synth, oracle_mod, dev, M, N, K, fused, timer, steps, 
     per = total / steps
     flops = 2.0 * M * N * K
     algo = wbytes + M * K * 2 + M * N * 2
+    vendor_us = None
+    if vendor and not fused:
+        # the vendor GEMM (torch.matmul -> hipBLASLt) on the same operands and rotation
+        vt, _ = timer.run(lambda i: torch.matmul(A, Bs[i % copies].t(), out=C), steps, warmup)
+        vendor_us = vt * 1e3 / steps
     res = dict(M=M, N=N, K=K, fused=fused, copies=copies, mode=mode,
                us_per_step=total * 1e3 / steps, us_kernel=per * 1e3,
                tflops_kernel=flops / (per * 1e-3) / 1e12,
                tflops_step=flops * steps / (total * 1e-3) / 1e12,
                gbs_kernel=algo / (per * 1e-3) / 1e9)
     res["mfma_frac_kernel"] = res["tflops_kernel"] / BF16_PEAK_TFLOPS
+    if vendor_us is not None:
+        res["vendor_us"] = vendor_us
+        res["vendor_tflops"] = flops / (vendor_us * 1e-6) / 1e12
     res["hbm_frac_kernel"] = res["gbs_kernel"] / HBM_PEAK_GBS
     torch.cuda.empty_cache()
     return res
@@ -277,6 +286,25 @@ def calib_copy(torch, dev):
     torch.cuda.synchronize()
 
 
+def launch_floors(torch, dev, timer, nbytes, steps):
+    """What one launch of this size costs in vendor kernels on the same box,
+    timed like the GEMV (HIP-graph replay, operands rotating over >= 1 GiB):
+    an empty launch (a 1-element fill), and torch's device copy moving the
+    same number of bytes (half read, half written)."""
+    tiny = torch.empty(1, device=dev)
+    t_fill, _ = timer.run(lambda i: tiny.zero_(), steps, 10)
+    half = nbytes // 2 // 4
+    copies = math.ceil(ROTATE_BYTES / (half * 4))
+    srcs = [torch.empty(half, dtype=torch.int32, device=dev) for _ in range(copies)]
+    dst = torch.empty(half, dtype=torch.int32, device=dev)
+    t_copy, _ = timer.run(lambda i: dst.copy_(srcs[i % copies]), steps, 10)
+    del srcs
+    torch.cuda.empty_cache()
+    return {"empty_launch_us": round(t_fill * 1e3 / steps, 3),
+            "torch_copy_same_bytes_us": round(t_copy * 1e3 / steps, 3),
+            "note": "vendor-kernel floors for one launch moving the GEMV's bytes"}
+
+
 def cpu_baseline(seconds):
     """The oracle's faithful per-element GEMV (src/main.cpp:73-84 restated)
     on the headline workload, single-threaded, repeated for ~`seconds`."""
@@ -327,7 +355,8 @@ def main():
     head = gemv_case(torch, ops, synth, dev, 4, 1, 8192, 2048, 64, torch.bfloat16,
                      timer, steps, warmup)
     gemm = gemm_case(torch, ops, synth, oracle, dev, 1024, 8192, 2048, False, timer,
-                     min(steps, 100), min(warmup, 10))
+                     min(steps, 100), min(warmup, 10), vendor=True)
+    floors = launch_floors(torch, dev, timer, head["bytes"], steps)
 
     out = {
         "metric": "4-bit GEMV HBM GB/s (% of 8 TB/s) at M=1; prefill GEMM TFLOP/s at M=1024",
@@ -353,7 +382,10 @@ def main():
         "gemm": {"workload": "bf16 GEMM M=1024 K=2048 N=8192, bf16 out",
                  "tflops": round(gemm["tflops_kernel"], 1),
                  "us": round(gemm["us_kernel"], 2),
-                 "frac_of_bf16_peak": round(gemm["mfma_frac_kernel"], 4)},
+                 "frac_of_bf16_peak": round(gemm["mfma_frac_kernel"], 4),
+                 "hipblaslt_us_same_operands": round(gemm["vendor_us"], 2),
+                 "hipblaslt_tflops": round(gemm["vendor_tflops"], 1)},
+        "gemv_floors": floors,
     }
     if args.calib_copy:
         calib_copy(torch, dev)

@@ -492,6 +492,9 @@ hipError_t by_group(uint32_t G, const void* X, const void* W, const void* S, con
 template <int MODE, int MT>
 hipError_t by_nt(int nt, uint32_t G, const void* X, const void* W, const void* S, const void* B,
                  void* Y, uint32_t M, uint32_t N, uint32_t K, int out_bf16, hipStream_t st) {
+    // (bf16 weights need 4x the load registers of a 4-bit n-tile: at most 2)
+    if constexpr (MODE != BF16)
+        if (nt >= 4) return by_group<MODE, MT, 4>(G, X, W, S, B, Y, M, N, K, out_bf16, st);
     if (nt >= 2) return by_group<MODE, MT, 2>(G, X, W, S, B, Y, M, N, K, out_bf16, st);
     return by_group<MODE, MT, 1>(G, X, W, S, B, Y, M, N, K, out_bf16, st);
 }
@@ -502,8 +505,11 @@ hipError_t by_shape(uint32_t G, const void* X, const void* W, const void* S, con
     // n-tiles per workgroup: x is loaded once per workgroup and reused by
     // each n-tile; two while that still gives >= 256 workgroups (more rows
     // per workgroup measured slower: fewer workgroups in flight)
+    // four for the 32-row products of a vocabulary-sized N, where x (M x K
+    // bf16, loaded once per workgroup) outweighs a 2-tile workgroup's weights
     int nt = (N >= 8192) ? 2 : 1;
-    if (const char* e = getenv("MIORI_SKINNY_NT")) nt = atoi(e) >= 2 ? 2 : 1;
+    if (M > 16 && N >= 65536) nt = 4;
+    if (const char* e = getenv("MIORI_SKINNY_NT")) nt = atoi(e);
     if (M <= 16) return by_nt<MODE, 1>(nt, G, X, W, S, B, Y, M, N, K, out_bf16, st);
     return by_nt<MODE, 2>(nt, G, X, W, S, B, Y, M, N, K, out_bf16, st);
 }
