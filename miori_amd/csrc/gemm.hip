@@ -59,9 +59,11 @@ struct Cfg {
     // two groups of the K tile; otherwise one bf16 in the low half)
     static constexpr int SB_W = 4;
     static constexpr int SB_ST = BN * SB_W;
+    // LDS ring depth: 3 stages, or 2 when three 256x256 stages would not fit
+    static constexpr int NST = (!Q4 && BM * BN > 256 * 128) ? 2 : 3;
     static constexpr int A_OFF = 0;
-    static constexpr int B_OFF = 3 * A_ST;          // bf16 B ring (3 stages)
-    static constexpr int RAW_OFF = B_OFF + 3 * B_ST;
+    static constexpr int B_OFF = NST * A_ST;        // bf16 B ring
+    static constexpr int RAW_OFF = B_OFF + NST * B_ST;
     static constexpr int S_OFF = RAW_OFF + 3 * RAW_ST;
     static constexpr int BI_OFF = S_OFF + 3 * SB_ST;
     static constexpr int LDS = Q4 ? BI_OFF + 3 * SB_ST : RAW_OFF;
@@ -72,7 +74,10 @@ struct Cfg {
     static constexpr int SB_INS = Q4 ? BN / 64 / 2 : 0;   // per wave (s or b), 64 rows each
     static constexpr int L = A_INS + B_INS + RAW_INS + SB_INS;
     static_assert(!Q4 || BN == 128, "fused dequant maps one thread per 32-code chunk");
-    static_assert(4 * WM * (WN + 8) * 4 <= LDS, "epilogue staging fits in the stage buffers");
+    // epilogue: each wave stages EPR rows of its fp32 tile at a time
+    static constexpr int EPR = (4 * WM * (WN + 8) * 4 <= LDS) ? WM : 32;
+    static_assert(4 * EPR * (WN + 8) * 4 <= LDS, "epilogue staging fits in the stage buffers");
+    static_assert(!Q4 || NST == 3, "the fused pipeline is written for three stages");
 };
 
 template <int BM, int BN, bool Q4, int G>
@@ -232,8 +237,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     const uint32_t lrow = (lane & 31u) * ROWB;
     auto read_frags = [&](uint32_t kt, int ks, int slot) {
         const uint32_t chunk = ((c0 ^ (uint32_t)ks) << 4) + lrow;
-        const uint32_t a_addr = CF::A_OFF + (kt % 3) * CF::A_ST + wm * CF::WM * ROWB + chunk;
-        const uint32_t b_addr = CF::B_OFF + (kt % 3) * CF::B_ST + wn * CF::WN * ROWB + chunk;
+        const uint32_t a_addr = CF::A_OFF + (kt % CF::NST) * CF::A_ST + wm * CF::WM * ROWB + chunk;
+        const uint32_t b_addr = CF::B_OFF + (kt % CF::NST) * CF::B_ST + wn * CF::WN * ROWB + chunk;
 #pragma unroll
         for (int i = 0; i < CF::TM; ++i)
             asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(af[slot][i]) : "v"(a_addr), "i"(i * 32 * ROWB));
@@ -322,6 +327,40 @@ __global__ __launch_bounds__(256) void gemm_kernel(
             mfmas((BK / 16 - 1) & 1);
             __builtin_amdgcn_sched_barrier(0);
         }
+    } else if constexpr (CF::NST == 2) {
+        // bf16, two stages: group kt+1 is the only one in flight during tile
+        // kt. The barrier of step kt (before its last k-step, whose fragments
+        // are already in registers) publishes group kt+1 and frees stage
+        // kt % 2, so group kt+2 is issued into it during that last k-step.
+        for (uint32_t kt = 0; kt < KT; ++kt) {
+            const bool dma = kt + 2 < KT;
+            read_frags(kt, 1, 1);
+            asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(NFR) : "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(0);
+            __builtin_amdgcn_sched_barrier(0);
+            read_frags(kt, 2, 0);
+            asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(NFR) : "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(1);
+            __builtin_amdgcn_sched_barrier(0);
+            read_frags(kt, 3, 1);
+            asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(NFR) : "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (kt + 1 < KT) {
+                wait_vm<0>();
+                barrier_lds();  // also completes the reads of the last k-step
+                read_frags(kt + 1, 0, 0);
+            } else {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            using I0 = std::integral_constant<int, 0>;
+            mfmas_dma(1, dma, kt + 2, kt % 2, I0{}, std::integral_constant<int, CF::L>{});
+            __builtin_amdgcn_sched_barrier(0);
+        }
     } else {
         // bf16: group kt+2 goes into stage (kt+2) % 3, freed by the barrier of
         // step kt-1, spread over k-steps 0..2 of tile kt. The barrier of step
@@ -366,25 +405,18 @@ __global__ __launch_bounds__(256) void gemm_kernel(
 
     // Epilogue through LDS (the stage buffers are free once every wave is past
     // the loop). Accumulator element e of lane l is row 8*(e/4) + 4*(l/32) +
-    // e%4, column l%32 of its 32x32 tile; each wave writes its WM x WN fp32
-    // tile to its own LDS region (row stride 72 floats: the two half-waves of
-    // a write land on disjoint banks), then reads it back 8 columns per lane
-    // and stores 16 bytes (bf16) or 2 x 16 bytes (fp32) per lane.
+    // e%4, column l%32 of its 32x32 tile. Each wave writes EPR rows of its
+    // WM x WN fp32 tile at a time to its own LDS region (row stride WN + 8
+    // floats: the two half-waves of a write land on disjoint banks), then
+    // reads them back 8 columns per lane and stores 16 bytes (bf16) or
+    // 2 x 16 bytes (fp32) per lane. Only this wave touches its region, and a
+    // wave's LDS accesses complete in order, so passes need no barrier.
     __syncthreads();
     constexpr uint32_t RS = CF::WN + 8;  // floats per LDS row
-    float* ep = reinterpret_cast<float*>(lds) + wave * (CF::WM * RS);
-#pragma unroll
-    for (int i = 0; i < CF::TM; ++i)
-#pragma unroll
-        for (int j = 0; j < CF::TN; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const uint32_t r = i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                ep[r * RS + j * 32 + (lane & 31u)] = acc[i][j][e];
-            }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    constexpr int EPR = CF::EPR;         // rows per pass
+    float* ep = reinterpret_cast<float*>(lds) + wave * (EPR * RS);
     constexpr uint32_t CPR = CF::WN / 8;          // 8-column chunks per row
-    constexpr uint32_t RPI = 64 / CPR;            // rows per pass
+    constexpr uint32_t RPI = 64 / CPR;            // rows per read-back iteration
     const uint32_t cc = lane % CPR, rr = lane / CPR;
     const uint32_t col = n0 + wn * CF::WN + cc * 8u;
     auto store8 = [&](uint32_t row, f32x4_t v0, f32x4_t v1) {
@@ -403,26 +435,42 @@ __global__ __launch_bounds__(256) void gemm_kernel(
             *reinterpret_cast<f32x4_t*>(dst + 4) = v1;
         }
     };
-    if (SK == 1) {
+    static_assert(CF::WM % EPR == 0 && EPR % 32 == 0, "passes cover whole 32-row MFMA tiles");
+#pragma unroll
+    for (int ps = 0; ps < CF::WM / EPR; ++ps) {
+#pragma unroll
+        for (int i = ps * (EPR / 32); i < (ps + 1) * (EPR / 32); ++i)
+#pragma unroll
+            for (int j = 0; j < CF::TN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const uint32_t r = (i - ps * (EPR / 32)) * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                    ep[r * RS + j * 32 + (lane & 31u)] = acc[i][j][e];
+                }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const uint32_t rbase = m0 + wm * CF::WM + ps * EPR;  // first output row of this pass
+        if (SK == 1) {
 #pragma unroll 4
-        for (uint32_t r = rr; r < CF::WM; r += RPI) {
-            const uint32_t row = m0 + wm * CF::WM + r;
-            const f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u);
-            const f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u + 4u);
-            if (row < M && col < N) store8(row, v0, v1);
+            for (uint32_t r = rr; r < (uint32_t)EPR; r += RPI) {
+                const uint32_t row = rbase + r;
+                const f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u);
+                const f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u + 4u);
+                if (row < M && col < N) store8(row, v0, v1);
+            }
+        } else {
+            // Split-K: the fp32 partial tile goes to part[ksp]; a second kernel
+            // adds the SK partials in split order (deterministic, and spread
+            // over every CU rather than funnelled through one workgroup per tile).
+            for (uint32_t r = rr; r < (uint32_t)EPR; r += RPI) {
+                const uint32_t row = rbase + r;
+                if (row >= M || col >= N) continue;
+                float* dst = part + ((size_t)ksp * M + row) * N + col;
+                *reinterpret_cast<f32x4_t*>(dst) = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u);
+                *reinterpret_cast<f32x4_t*>(dst + 4) = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u + 4u);
+            }
         }
-        return;
-    }
-
-    // Split-K: the fp32 partial tile goes to part[ksp]; a second kernel adds
-    // the SK partials in split order (deterministic, and spread over every
-    // CU rather than funnelled through one workgroup per tile).
-    for (uint32_t r = rr; r < CF::WM; r += RPI) {
-        const uint32_t row = m0 + wm * CF::WM + r;
-        if (row >= M || col >= N) continue;
-        float* dst = part + ((size_t)ksp * M + row) * N + col;
-        *reinterpret_cast<f32x4_t*>(dst) = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u);
-        *reinterpret_cast<f32x4_t*>(dst + 4) = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u + 4u);
+        // the next pass rewrites this region: its reads must have returned
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
 }
 
@@ -525,11 +573,18 @@ uint32_t pick_split(uint32_t tiles, uint32_t KT, uint64_t MN) {
 hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* s,
                        const void* b, void* C, uint32_t M, uint32_t N, uint32_t K,
                        uint32_t G, int out_bf16, hipStream_t st) {
-    // 256x128 tiles when they come in whole waves of 256 (one per CU);
-    // otherwise 128x128 tiles with K split over workgroups to fill the chip.
+    // bf16 weight cache: 256x256 tiles (128 flop per operand byte, against
+    // 85 for 256x128) once they fill at least 3/4 of the 256 CUs in a round;
+    // the split-K cost model is not applied to them (SK = 1).
+    // Otherwise 256x128 tiles when they come in whole waves of 256 (one per
+    // CU), else 128x128 tiles with K split over workgroups to fill the chip.
+    const uint64_t huge = (uint64_t)((M + 255) / 256) * ((N + 255) / 256);
     const uint64_t big = (uint64_t)((M + 255) / 256) * ((N + 127) / 128);
     int tile = (big >= 256 && big % 256 == 0) ? 0 : 1;
+    if (!q && huge >= 192) tile = 2;
     if (const char* e = getenv("MIORI_GEMM_TILE")) tile = atoi(e);
+    if (tile == 2 && !q) return launch_cfg<256, 256, false, 64>(A, B, q, s, b, C, M, N, K, out_bf16, 1, st);
+    if (tile == 2) tile = (big >= 256 && big % 256 == 0) ? 0 : 1;  // fused: no 256x256 variant
     const uint32_t ntiles = tile == 0 ? (uint32_t)big : ((M + 127) / 128) * ((N + 127) / 128);
     // partial traffic from the padded tile grid, so every M in one row-tile
     // count splits alike (rows of a small product equal those of a larger one)
