@@ -196,18 +196,42 @@ LAYER = [("q", 2048, 2048), ("k", 2048, 512), ("v", 2048, 512), ("o", 2048, 2048
          ("gate", 2048, 8192), ("up", 2048, 8192), ("down", 8192, 2048)]
 
 
-def chain_case(torch, ops, synth, dev, M, timer, layers=24, G=64, steps=3, warmup=1):
+class _Stacked:
+    """Row-stacked weights of projections that read the same activation
+    (q|k|v, gate|up): one product of N = sum of the parts, the same values
+    per output row as the separate products."""
+
+    def __init__(self, torch, lins):
+        self.q = torch.cat([l.q for l in lins], 0)
+        self.s = torch.cat([l.s for l in lins], 0)
+        self.b = torch.cat([l.b for l in lins], 0)
+
+
+def chain_case(torch, ops, synth, dev, M, timer, layers=24, G=64, steps=3, warmup=1,
+               stacked=False):
     """Config 4: the fused 4-bit GEMM over a synthetic 24-layer projection
     chain (7 projections per layer, distinct random weights per layer), M
-    activation rows. One step = the whole chain (168 GEMMs)."""
+    activation rows. One step = the whole chain: 168 GEMMs, or with
+    `stacked` 96, q|k|v and gate|up each one product on row-stacked weights
+    (they read the same activation), as an engine lays them out."""
     ws = []
     for l in range(layers):
+        lins = []
         for i, (name, K, N) in enumerate(LAYER):
             w = synth.quant_weights(N, K, G, 4, seed=synth.BASE_SEED + 1000 * l + i)
-            ws.append((ops.QuantLinear(w, dev), K, N))
+            lins.append((ops.QuantLinear(w, dev), K, N))
+        if stacked:
+            ws.append((_Stacked(torch, [x[0] for x in lins[0:3]]), 2048, 3072))
+            ws.append(lins[3])
+            ws.append((_Stacked(torch, [x[0] for x in lins[4:6]]), 2048, 16384))
+            ws.append(lins[6])
+            del lins
+        else:
+            ws.extend(lins)
     a2 = ops.to_device_bits(synth.activations(M, 2048), dev)
     a8 = ops.to_device_bits(synth.activations(M, 8192), dev)
-    outs = {N: torch.empty((M, N), dtype=torch.bfloat16, device=dev) for N in (512, 2048, 8192)}
+    outs = {N: torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            for N in (512, 2048, 3072, 8192, 16384)}
 
     def fn(i):
         for lin, K, N in ws:
@@ -217,7 +241,8 @@ def chain_case(torch, ops, synth, dev, M, timer, layers=24, G=64, steps=3, warmu
     per = total / steps
     flops = sum(2.0 * M * N * K for _, K, N in ws)
     wbytes = sum(l.q.numel() * 4 + l.s.numel() * 2 + l.b.numel() * 2 for l, _, _ in ws)
-    res = dict(config=4, M=M, layers=layers, gemms=len(ws), mode=mode, us_per_chain=per * 1e3,
+    res = dict(config=4, M=M, layers=layers, gemms=len(ws), stacked=stacked, mode=mode,
+               us_per_chain=per * 1e3,
                tflops=flops / (per * 1e-3) / 1e12, weight_gbs=wbytes / (per * 1e-3) / 1e9,
                weight_bytes=wbytes, flops=flops)
     res["mfma_frac"] = res["tflops"] / BF16_PEAK_TFLOPS
@@ -411,8 +436,9 @@ def run_all(torch, ops, synth, oracle, dev, timer):
                                                torch.bfloat16, timer, 20, 3)))
         print(f"[bench] {rows[-1]}", file=sys.stderr, flush=True)
     for M in (1024, 32):
-        rows.append(chain_case(torch, ops, synth, dev, M, timer))
-        print(f"[bench] {rows[-1]}", file=sys.stderr, flush=True)
+        for stacked in (False, True):
+            rows.append(chain_case(torch, ops, synth, dev, M, timer, stacked=stacked))
+            print(f"[bench] {rows[-1]}", file=sys.stderr, flush=True)
     for fused in (False, True):
         for M in (256, 1024, 1472):
             for (K, N) in [(2048, 8192), (8192, 2048), (2048, 2560)]:
