@@ -247,6 +247,22 @@ __global__ __launch_bounds__(256) void gemm_kernel(
             asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(bf[slot][j]) : "v"(b_addr), "i"(j * 32 * ROWB));
     };
     constexpr int NFR = CF::TM + CF::TN;  // LDS reads per k-step
+    // With 8 reads per k-step a full double buffer would put 16 reads in
+    // flight, more than the 4-bit lgkm counter holds (15). This variant
+    // issues the A fragments of the next k-step, waits until only they are
+    // outstanding (the previous slot has landed), then issues the B ones.
+    auto read_frags_capped = [&](uint32_t kt, int ks, int slot) {
+        const uint32_t chunk = ((c0 ^ (uint32_t)ks) << 4) + lrow;
+        const uint32_t a_addr = CF::A_OFF + (kt % CF::NST) * CF::A_ST + wm * CF::WM * ROWB + chunk;
+        const uint32_t b_addr = CF::B_OFF + (kt % CF::NST) * CF::B_ST + wn * CF::WN * ROWB + chunk;
+#pragma unroll
+        for (int i = 0; i < CF::TM; ++i)
+            asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(af[slot][i]) : "v"(a_addr), "i"(i * 32 * ROWB));
+        asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(CF::TM) : "memory");
+#pragma unroll
+        for (int j = 0; j < CF::TN; ++j)
+            asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(bf[slot][j]) : "v"(b_addr), "i"(j * 32 * ROWB));
+    };
     auto mfmas = [&](int slot) {
 #pragma unroll
         for (int i = 0; i < CF::TM; ++i)
@@ -334,18 +350,15 @@ __global__ __launch_bounds__(256) void gemm_kernel(
         // kt % 2, so group kt+2 is issued into it during that last k-step.
         for (uint32_t kt = 0; kt < KT; ++kt) {
             const bool dma = kt + 2 < KT;
-            read_frags(kt, 1, 1);
-            asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(NFR) : "memory");
+            read_frags_capped(kt, 1, 1);
             __builtin_amdgcn_sched_barrier(0);
             mfmas(0);
             __builtin_amdgcn_sched_barrier(0);
-            read_frags(kt, 2, 0);
-            asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(NFR) : "memory");
+            read_frags_capped(kt, 2, 0);
             __builtin_amdgcn_sched_barrier(0);
             mfmas(1);
             __builtin_amdgcn_sched_barrier(0);
-            read_frags(kt, 3, 1);
-            asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(NFR) : "memory");
+            read_frags_capped(kt, 3, 1);
             __builtin_amdgcn_sched_barrier(0);
             mfmas(0);
             __builtin_amdgcn_sched_barrier(0);
