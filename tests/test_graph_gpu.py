@@ -1,0 +1,104 @@
+"""HIP-graph capture of every entry-point family (the benchmark times all of
+them as graph replays): each call is made eagerly once (which also sizes the
+split-K workspace outside capture), captured into a graph, and the graph is
+replayed three times. Between replays the output is cleared and other eager
+work runs on the same stream, including an eager split-K product that uses
+the same per-device workspace. Every replay must reproduce the eager result
+bit for bit."""
+import numpy as np
+import pytest
+import torch
+
+from miori_amd import ops, synth
+from tests.gpu_util import acts, say, weights
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(name, dev):
+    """(launch function, output tensor) for one entry point."""
+    if name == "gemv4":
+        _, lin = weights(8192, 2048, 64, 4, seed=11, dev=dev)
+        _, x = acts(1, 2048, seed=12, dev=dev)
+        y = torch.empty(8192, dtype=torch.bfloat16, device=dev)
+        return (lambda: ops.gemv4(lin.q, lin.s, lin.b, x, y, 8192, 2048)), y
+    if name == "gemv8":
+        _, lin = weights(4096, 2048, 64, 8, seed=13, dev=dev)
+        _, x = acts(1, 2048, seed=14, dev=dev)
+        y = torch.empty(4096, dtype=torch.float32, device=dev)
+        return (lambda: ops.gemv8(lin.q, lin.s, lin.b, x, y, 4096, 2048)), y
+    if name.startswith("gemv4_b"):
+        M = int(name.split("_m")[1])
+        _, lin = weights(2048, 2048, 64, 4, seed=15 + M, dev=dev)
+        _, x = acts(M, 2048, seed=16 + M, dev=dev)
+        y = torch.empty((M, 2048), dtype=torch.bfloat16, device=dev)
+        return (lambda: ops.gemv4_b(lin.q, lin.s, lin.b, x, y, 2048, 2048, M)), y
+    if name.startswith("gemm_bf16"):
+        M, N, K = {"gemm_bf16_splitk": (256, 2560, 2048), "gemm_bf16_256": (1472, 8192, 2048),
+                   "gemm_bf16_skinny": (24, 2048, 2048)}[name]
+        _, A = acts(M, K, seed=17, dev=dev)
+        B = (torch.randn(N, K, device=dev) * 0.05).to(torch.bfloat16)
+        C = torch.empty((M, N), dtype=torch.float32, device=dev)
+        return (lambda: ops.gemm_mpp(A, B, C, M, N, K)), C
+    if name == "gemm_q4":
+        M, N, K = 1024, 2048, 2048
+        _, lin = weights(N, K, 64, 4, seed=18, dev=dev)
+        _, A = acts(M, K, seed=19, dev=dev)
+        C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        return (lambda: ops.gemm_q4(A, lin.q, lin.s, lin.b, C, M, N, K)), C
+    if name == "gemm_naive":
+        M, N, K = 32, 16, 2048
+        _, A = acts(M, K, seed=20, dev=dev)
+        B = (torch.randn(N, K, device=dev) * 0.05).to(torch.bfloat16)
+        C = torch.empty((M, N), dtype=torch.float32, device=dev)
+        return (lambda: ops.gemm_naive(A, B, C, M, N, K, K, K, N)), C
+    if name == "rmsnorm_gemv4":
+        _, lin = weights(2048, 2048, 64, 4, seed=21, dev=dev)
+        x = torch.randn(2048, device=dev)
+        nw = (torch.rand(2048, device=dev) + 0.5).to(torch.bfloat16)
+        y = torch.empty(2048, dtype=torch.float32, device=dev)
+        return (lambda: ops.rmsnorm_gemv4(x, nw, lin.q, lin.s, lin.b, y, 2048, 2048)), y
+    if name == "silu_mul_gemv4":
+        _, lin = weights(2048, 2048, 64, 4, seed=22, dev=dev)
+        g = torch.randn(2048, device=dev)
+        u = torch.randn(2048, device=dev)
+        y = torch.empty(2048, dtype=torch.float32, device=dev)
+        return (lambda: ops.silu_mul_gemv4(g, u, lin.q, lin.s, lin.b, y, 2048, 2048)), y
+    if name == "dequant_tile":
+        _, lin = weights(2048, 2048, 64, 4, seed=23, dev=dev)
+        out = torch.empty((2048, 2048), dtype=torch.bfloat16, device=dev)
+        return (lambda: ops.dequant_tile(lin.q, lin.s, lin.b, out, 2048, 2048)), out
+    raise KeyError(name)
+
+
+CASES = ["gemv4", "gemv8", "gemv4_b_m4", "gemv4_b_m8", "gemv4_b_m32", "gemm_bf16_splitk",
+         "gemm_bf16_256", "gemm_bf16_skinny", "gemm_q4", "gemm_naive", "rmsnorm_gemv4",
+         "silu_mul_gemv4", "dequant_tile"]
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_graph_replay_matches_eager(dev, name):
+    say(f"graph replay {name}")
+    fn, out = _case(name, dev)
+    # unrelated eager work between replays: a torch product and an eager
+    # split-K GEMM sharing the library's workspace
+    xa = torch.randn(512, 512, device=dev)
+    _, A2 = acts(256, 2048, seed=99, dev=dev)
+    B2 = (torch.randn(2560, 2048, device=dev) * 0.05).to(torch.bfloat16)
+    C2 = torch.empty((256, 2560), dtype=torch.float32, device=dev)
+    ops.gemm_mpp(A2, B2, C2, 256, 2560, 2048)
+    fn()
+    torch.cuda.synchronize()
+    ref = ops.bits_of(out).copy()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    for r in range(3):
+        out.zero_()
+        _ = xa @ xa
+        ops.gemm_mpp(A2, B2, C2, 256, 2560, 2048)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(ops.bits_of(out), ref, err_msg=f"{name} replay {r}")
