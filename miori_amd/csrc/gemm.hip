@@ -524,6 +524,17 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
     }
 }
 
+}  // namespace
+
+hipError_t launch_splitk_reduce(const float* part, void* C, size_t MN, uint32_t SK, int out_bf16,
+                                hipStream_t st) {
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((MN / 8 + 255) / 256)), dim3(256), 0,
+                       st, part, C, MN, SK, out_bf16);
+    return hipGetLastError();
+}
+
+namespace {
+
 template <int BM, int BN, bool Q4, int G>
 hipError_t launch_cfg(const void* A, const void* B, const void* q, const void* s, const void* b,
                       void* C, uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t SK,
@@ -542,9 +553,9 @@ hipError_t launch_cfg(const void* A, const void* B, const void* q, const void* s
                        (const uint16_t*)s, (const uint16_t*)b, C, M, N, K, out_bf16, tiles_m,
                        remap, part, SK, ntiles);
     if (SK > 1) {
-        const size_t MN = (size_t)M * N;
-        hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((MN / 8 + 255) / 256)), dim3(256), 0,
-                           st, (const float*)part, C, MN, SK, out_bf16);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_splitk_reduce(part, C, (size_t)M * N, SK, out_bf16, st);
     }
     return hipGetLastError();
 }

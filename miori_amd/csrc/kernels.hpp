@@ -45,5 +45,9 @@ hipError_t launch_skinny(int mode, const void* X, const void* W, const void* S, 
 
 // Split-K partials workspace of the current device (grown outside graph capture).
 hipError_t workspace_get(hipStream_t st, size_t bytes, float** part);
+// C[i] = sum over k = 0..SK-1 of part[k * MN + i], in that order, as fp32 or
+// bf16 (MN a multiple of 8).
+hipError_t launch_splitk_reduce(const float* part, void* C, size_t MN, uint32_t SK, int out_bf16,
+                                hipStream_t st);
 
 }  // namespace miori

@@ -11,10 +11,12 @@
 //   BF16 bf16 weight cache (gemm_mpp at small M)
 //
 // Structure (v_mfma_f32_16x16x32_bf16; x is the A operand, W^T the B one):
-//  * A workgroup of 8 waves owns 16*NT output rows; the waves split K, each
-//    taking a contiguous run of at most 8 128-wide K blocks (64 for 8-bit),
-//    and the eight partial tiles meet in LDS at the end (fixed order). No K
-//    split across workgroups: one pass, one store.
+//  * A workgroup of 8 waves owns 16*NT output rows and 1/SK of K; the waves
+//    split its K range, each taking a contiguous run of at most 8 128-wide K
+//    blocks (64 for 8-bit), and the eight partial tiles meet in LDS at the
+//    end (fixed order). SK = 1: one pass, one store. SK > 1 (split over
+//    gridDim.y, for products whose activation rows outweigh a workgroup's
+//    weights): fp32 partials, added in split order by a second kernel.
 //  * Weights go straight from memory to registers, 16 bytes per lane: lane
 //    (row n = lane % 16, quarter c = lane / 16) loads 32 codes (4-bit) or 16
 //    codes (8-bit) of row n. The MFMA sums over the 32 k of a step, so the k
@@ -65,7 +67,9 @@ struct Sk {
     // scale / bias tiles of the workgroup's rows in LDS (all K/G groups of up
     // to NBW * NW blocks), rounded up to whole 1 KiB DMA chunks
     static constexpr int NB = 16 * NT;
-    static constexpr int NGMAX = EXACT || MODE == Q4F ? (NBW * NW * KB) / G : 0;
+    // (all K / G groups of a row: sized for the largest supported K, 8 blocks
+    // per wave, so a workgroup of a K split indexes groups absolutely)
+    static constexpr int NGMAX = EXACT || MODE == Q4F ? (8 * NW * KB) / G : 0;
     // (+ room for the masked reads of padding blocks past a row's end)
     static constexpr int SB_BYTES = ((NB * NGMAX * 2 + NBW * KB / 16 + 1023) / 1024) * 1024;
     static constexpr int RED_BYTES = NW * TOT * 4;
@@ -170,7 +174,7 @@ template <int MODE, int MT, int NT, int G, int NBW>
 __global__ __launch_bounds__(NW * 64) void skinny_kernel(
     const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
     const uint16_t* __restrict__ S, const uint16_t* __restrict__ Bi, void* __restrict__ Y,
-    uint32_t M, uint32_t N, uint32_t K, int out_bf16) {
+    uint32_t M, uint32_t N, uint32_t K, int out_bf16, float* __restrict__ part) {
     using C = Sk<MODE, MT, NT, G, NBW>;
     // scale / bias tiles first, the cross-wave reduction buffer at the end
     __shared__ __attribute__((aligned(1024))) uint8_t lds[C::LDS];
@@ -185,7 +189,9 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
     const uint32_t j = lane & 15u, c = lane >> 4;
     const uint32_t n0 = blockIdx.x * 16u * NT;
     const uint32_t nblk = K / C::KB;
-    const uint32_t b0 = wave * nblk / NW, b1 = (wave + 1) * nblk / NW;
+    // this workgroup's K blocks: [kb0, kb0 + nloc) (split gridDim.y ways)
+    const uint32_t nloc = nblk / gridDim.y, kb0 = blockIdx.y * nloc;
+    const uint32_t b0 = kb0 + wave * nloc / NW, b1 = kb0 + (wave + 1) * nloc / NW;
     const uint32_t nb = b1 - b0;
     const uint32_t ng = (MODE == BF16) ? 1u : K / G;
 
@@ -442,17 +448,33 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
         const uint32_t nt = tm / MT, mt = tm % MT;
         const uint32_t n = n0 + nt * 16u + (ln & 15u);
         const uint32_t m = mt * 16u + 4u * (ln >> 4) + e4;
-        if (n < N && m < M) store_out(Y, (size_t)m * N + n, v, bf);
+        if (n < N && m < M) {
+            if (gridDim.y == 1)
+                store_out(Y, (size_t)m * N + n, v, bf);
+            else
+                part[((size_t)blockIdx.y * M + m) * N + n] = v;
+        }
     }
 }
 
 template <int MODE, int MT, int NT, int G, int NBW>
 hipError_t launch_sk(const void* X, const void* W, const void* S, const void* B, void* Y,
-                     uint32_t M, uint32_t N, uint32_t K, int out_bf16, hipStream_t st) {
+                     uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t SK,
+                     hipStream_t st) {
     const uint32_t nwg = (N + 16 * NT - 1) / (16 * NT);
-    hipLaunchKernelGGL((skinny_kernel<MODE, MT, NT, G, NBW>), dim3(nwg), dim3(NW * 64), 0, st,
+    float* part = nullptr;
+    if (SK > 1) {
+        const hipError_t e = workspace_get(st, (size_t)SK * M * N * 4, &part);
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL((skinny_kernel<MODE, MT, NT, G, NBW>), dim3(nwg, SK), dim3(NW * 64), 0, st,
                        (const uint16_t*)X, (const uint8_t*)W, (const uint16_t*)S,
-                       (const uint16_t*)B, Y, M, N, K, out_bf16);
+                       (const uint16_t*)B, Y, M, N, K, out_bf16, part);
+    if (SK > 1) {
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_splitk_reduce(part, Y, (size_t)M * N, SK, out_bf16, st);
+    }
     return hipGetLastError();
 }
 
@@ -464,25 +486,26 @@ inline int nbw_of(uint32_t K, uint32_t kb) {
 
 template <int MODE, int MT, int NT, int G>
 hipError_t by_nbw(const void* X, const void* W, const void* S, const void* B, void* Y,
-                  uint32_t M, uint32_t N, uint32_t K, int out_bf16, hipStream_t st) {
-    switch (nbw_of(K, MODE == Q8X ? 64u : 128u)) {
-        case 1: return launch_sk<MODE, MT, NT, G, 1>(X, W, S, B, Y, M, N, K, out_bf16, st);
-        case 2: return launch_sk<MODE, MT, NT, G, 2>(X, W, S, B, Y, M, N, K, out_bf16, st);
-        case 4: return launch_sk<MODE, MT, NT, G, 4>(X, W, S, B, Y, M, N, K, out_bf16, st);
+                  uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t SK, hipStream_t st) {
+    switch (nbw_of(K / SK, MODE == Q8X ? 64u : 128u)) {
+        case 1: return launch_sk<MODE, MT, NT, G, 1>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
+        case 2: return launch_sk<MODE, MT, NT, G, 2>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
+        case 4: return launch_sk<MODE, MT, NT, G, 4>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
     }
-    return launch_sk<MODE, MT, NT, G, 8>(X, W, S, B, Y, M, N, K, out_bf16, st);
+    return launch_sk<MODE, MT, NT, G, 8>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
 }
 
 template <int MODE, int MT, int NT>
 hipError_t by_group(uint32_t G, const void* X, const void* W, const void* S, const void* B,
-                    void* Y, uint32_t M, uint32_t N, uint32_t K, int out_bf16, hipStream_t st) {
+                    void* Y, uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t SK,
+                    hipStream_t st) {
     if constexpr (MODE == BF16) {
-        return by_nbw<BF16, MT, NT, 64>(X, W, S, B, Y, M, N, K, out_bf16, st);
+        return by_nbw<BF16, MT, NT, 64>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
     } else {
         switch (G) {
-            case 32: return by_nbw<MODE, MT, NT, 32>(X, W, S, B, Y, M, N, K, out_bf16, st);
-            case 64: return by_nbw<MODE, MT, NT, 64>(X, W, S, B, Y, M, N, K, out_bf16, st);
-            case 128: return by_nbw<MODE, MT, NT, 128>(X, W, S, B, Y, M, N, K, out_bf16, st);
+            case 32: return by_nbw<MODE, MT, NT, 32>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
+            case 64: return by_nbw<MODE, MT, NT, 64>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
+            case 128: return by_nbw<MODE, MT, NT, 128>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
         }
         return hipErrorInvalidValue;
     }
@@ -491,12 +514,13 @@ hipError_t by_group(uint32_t G, const void* X, const void* W, const void* S, con
 // (an element's k order and wave reduction do not depend on NT)
 template <int MODE, int MT>
 hipError_t by_nt(int nt, uint32_t G, const void* X, const void* W, const void* S, const void* B,
-                 void* Y, uint32_t M, uint32_t N, uint32_t K, int out_bf16, hipStream_t st) {
+                 void* Y, uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t SK,
+                 hipStream_t st) {
     // (bf16 weights need 4x the load registers of a 4-bit n-tile: at most 2)
     if constexpr (MODE != BF16)
-        if (nt >= 4) return by_group<MODE, MT, 4>(G, X, W, S, B, Y, M, N, K, out_bf16, st);
-    if (nt >= 2) return by_group<MODE, MT, 2>(G, X, W, S, B, Y, M, N, K, out_bf16, st);
-    return by_group<MODE, MT, 1>(G, X, W, S, B, Y, M, N, K, out_bf16, st);
+        if (nt >= 4) return by_group<MODE, MT, 4>(G, X, W, S, B, Y, M, N, K, out_bf16, SK, st);
+    if (nt >= 2) return by_group<MODE, MT, 2>(G, X, W, S, B, Y, M, N, K, out_bf16, SK, st);
+    return by_group<MODE, MT, 1>(G, X, W, S, B, Y, M, N, K, out_bf16, SK, st);
 }
 
 template <int MODE>
@@ -505,13 +529,31 @@ hipError_t by_shape(uint32_t G, const void* X, const void* W, const void* S, con
     // n-tiles per workgroup: x is loaded once per workgroup and reused by
     // each n-tile; two while that still gives >= 256 workgroups (more rows
     // per workgroup measured slower: fewer workgroups in flight)
-    // four for the 32-row products of a vocabulary-sized N, where x (M x K
-    // bf16, loaded once per workgroup) outweighs a 2-tile workgroup's weights
+    // four for the 32-row products of N >= 16384, where x (M x K bf16, loaded
+    // once per workgroup) outweighs a 2-tile workgroup's weights
     int nt = (N >= 8192) ? 2 : 1;
-    if (M > 16 && N >= 65536) nt = 4;
+    if (M > 16 && N >= 16384) nt = 4;
+    // K split over workgroups for K >= 8192 at M > 8: a workgroup then loads
+    // a quarter of x (M x 8192 bf16 is 512 KB at M = 32, against 64 KB of
+    // its weights), and the fp32 partials are added by a second kernel.
+    // Measured (N = 2048, K = 8192): M=32 19.3 -> 12.2 us, M=16 12.0 -> 10.4;
+    // at M = 8 and at K = 2048 the split was slower.
+    uint32_t sk = 1;
+    if (M > 8 && K >= 8192) {
+        sk = 4;
+        nt = 2;
+    }
     if (const char* e = getenv("MIORI_SKINNY_NT")) nt = atoi(e);
-    if (M <= 16) return by_nt<MODE, 1>(nt, G, X, W, S, B, Y, M, N, K, out_bf16, st);
-    return by_nt<MODE, 2>(nt, G, X, W, S, B, Y, M, N, K, out_bf16, st);
+    // N a multiple of 16 so the partials' reduction covers whole 8-element
+    // groups; the split must divide the K blocks
+    if (const char* e = getenv("MIORI_SKINNY_SPLIT")) sk = (uint32_t)atoi(e);
+    const uint32_t kb = MODE == Q8X ? 64u : 128u;
+    if (sk < 1 || N % 16 != 0) sk = 1;
+    // (a function of N and K only, so the fused 4-bit and the bf16 products
+    // of one shape split alike and stay bit-identical)
+    while (sk > 1 && (K / kb) % sk != 0) --sk;
+    if (M <= 16) return by_nt<MODE, 1>(nt, G, X, W, S, B, Y, M, N, K, out_bf16, sk, st);
+    return by_nt<MODE, 2>(nt, G, X, W, S, B, Y, M, N, K, out_bf16, sk, st);
 }
 
 }  // namespace
