@@ -276,7 +276,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     // the matrix core is busy instead of stalling on a burst of them.
     constexpr int NM = CF::TM * CF::TN;
     constexpr int PER = (CF::L + 2) / 3;  // DMA instructions per k-step (k-steps 0..2)
-    static_assert(Q4 || PER <= NM, "one DMA per MFMA at most");
+    // (small tiles have fewer MFMAs than DMA instructions per k-step: then
+    // several DMAs follow one MFMA)
     auto mfmas_dma = [&](int slot, bool dma, uint32_t dkt, uint32_t dst, auto p0c, auto p1c) {
         constexpr int P0 = decltype(p0c)::value, P1 = decltype(p1c)::value;
         constexpr int CNT = P1 - P0;
@@ -286,8 +287,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][i], bf[slot][j],
                                                                 acc[i][j], 0, 0, 0);
             if constexpr (CNT > 0) {
-                if ((q * CNT) / NM != ((q + 1) * CNT) / NM && dma)
-                    issue_one(dkt, dst, P0 + (q * CNT) / NM);
+                // DMAs [P0 + q*CNT/NM, P0 + (q+1)*CNT/NM) after MFMA q
+#pragma unroll
+                for (int p = (q * CNT) / NM; p < ((q + 1) * CNT) / NM; ++p)
+                    if (dma) issue_one(dkt, dst, P0 + p);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -597,28 +600,44 @@ uint32_t pick_split(uint32_t tiles, uint32_t KT, uint64_t MN) {
 hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* s,
                        const void* b, void* C, uint32_t M, uint32_t N, uint32_t K,
                        uint32_t G, int out_bf16, hipStream_t st) {
-    // bf16 weight cache: 256x256 tiles (128 flop per operand byte, against
-    // 85 for 256x128) once they fill at least 3/4 of the 256 CUs in a round;
-    // the split-K cost model is not applied to them (SK = 1).
-    // Otherwise 256x128 tiles when they come in whole waves of 256 (one per
-    // CU), else 128x128 tiles with K split over workgroups to fill the chip.
+    // Tile choice (MIORI_GEMM_TILE overrides: 0 = 256x128, 1 = 128x128,
+    // 2 = 256x256, 3 = 64x128, 4 = 64x64):
+    //  * bf16 weight cache: 256x256 tiles (128 flop per operand byte, against
+    //    85 for 256x128) once they fill at least 3/4 of the 256 CUs in a
+    //    round; the split-K cost model is not applied to them (SK = 1).
+    //  * small grids (K <= 4096, at most 512 64x64 tiles): 64x64 tiles (bf16)
+    //    or 64x128 (fused 4-bit), 2-3 workgroups per CU. Both paths take the
+    //    K split the cost model picks for the 64x128 grid (usually none), so
+    //    fused and bf16 products stay bit-identical. Measured against
+    //    128x128 tiles with split partials: bf16 M=1024 N=2048 19.7 -> 15.0
+    //    us, M=256 N=8192 19.9 -> 15.3 us; fused M=1024 N=512 25.8 -> 16.7.
+    //  * otherwise 256x128 tiles when they come in whole waves of 256 (one
+    //    per CU), else 128x128 tiles with K split over workgroups to fill
+    //    the chip.
     const uint64_t huge = (uint64_t)((M + 255) / 256) * ((N + 255) / 256);
     const uint64_t big = (uint64_t)((M + 255) / 256) * ((N + 127) / 128);
+    const uint64_t t64 = (uint64_t)((M + 63) / 64) * ((N + 63) / 64);
     int tile = (big >= 256 && big % 256 == 0) ? 0 : 1;
     if (!q && huge >= 192) tile = 2;
+    else if (K <= 4096 && t64 <= 512) tile = q ? 3 : 4;
     if (const char* e = getenv("MIORI_GEMM_TILE")) tile = atoi(e);
     if (tile == 2 && !q) return launch_cfg<256, 256, false, 64>(A, B, q, s, b, C, M, N, K, out_bf16, 1, st);
     if (tile == 2) tile = (big >= 256 && big % 256 == 0) ? 0 : 1;  // fused: no 256x256 variant
-    const uint32_t ntiles = tile == 0 ? (uint32_t)big : ((M + 127) / 128) * ((N + 127) / 128);
+    // (64x64 splits as the 64x128 grid, the fused path's tile)
+    const uint32_t tbm = tile == 0 ? 256 : (tile == 3 || tile == 4) ? 64 : 128;
+    const uint32_t tbn = 128;
+    const uint32_t ntiles = ((M + tbm - 1) / tbm) * ((N + tbn - 1) / tbn);
     // partial traffic from the padded tile grid, so every M in one row-tile
     // count splits alike (rows of a small product equal those of a larger one)
-    const uint64_t tile_elems = tile == 0 ? 256 * 128 : 128 * 128;
+    const uint64_t tile_elems = (uint64_t)tbm * tbn;
     uint32_t SK = pick_split(ntiles, K / 64, ntiles * tile_elems);
     if (const char* e = getenv("MIORI_GEMM_SPLIT")) SK = (uint32_t)atoi(e);
     if (SK < 1) SK = 1;
     if (SK > 16) SK = 16;
     if (SK > K / 64) SK = K / 64;
     if (tile == 0) return launch_tile<256, 128>(A, B, q, s, b, C, M, N, K, G, out_bf16, SK, st);
+    if (tile == 3) return launch_tile<64, 128>(A, B, q, s, b, C, M, N, K, G, out_bf16, SK, st);
+    if (tile == 4 && !q) return launch_cfg<64, 64, false, 64>(A, B, q, s, b, C, M, N, K, out_bf16, SK, st);
     return launch_tile<128, 128>(A, B, q, s, b, C, M, N, K, G, out_bf16, SK, st);
 }
 
