@@ -38,6 +38,7 @@
 
 #include <stdlib.h>
 
+#include <algorithm>
 #include <type_traits>
 
 namespace miori {
@@ -457,11 +458,239 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
     }
 }
 
+// Register budget of the persistent kernel: x of all NBW blocks, one weight
+// slot per block and the accumulators stay live across the tile loop (in
+// 4-byte registers; G = 32's extra word exchange costs more). Instances over
+// the bound were measured to spill.
+constexpr bool persist_fits(int mode, int mt, int nt, int g, int nbw) {
+    const int steps = mode == Q8X ? 2 : 4;
+    return (mode == Q4X || mode == Q8X) && nbw <= 4 &&
+           nbw * mt * steps * 4 + nbw * nt * 4 + nt * mt * 4 + (g == 32 ? 48 : 0) <= 88;
+}
+
+// Persistent variant for vocabulary-sized N (exact modes Q4X / Q8X, no K
+// split): each workgroup loops over row tiles t = blockIdx.x, + gridDim.x,
+// ... . Per tile it computes what skinny_kernel computes for one workgroup
+// (the same blocks per wave, per-element k order and wave reduction, so the
+// results are identical), with two differences:
+//  * x (this wave's NBW K blocks) is loaded into registers once, not once per
+//    tile: at M = 32, K = 2048 that is 128 KB per workgroup saved per tile;
+//  * after block i of tile t is computed, the weights, scales and biases of
+//    block i of the next tile are loaded into the same registers, so the
+//    next tile's loads are in flight while this tile finishes, is reduced
+//    and is stored.
+// Every load here is compiler code (no inline-asm loads, no hand-placed
+// waits): the loads the loop carries into its next iteration are waited for
+// by the compiler wherever their registers are used or copied.
+template <int MODE, int MT, int NT, int G, int NBW>
+__global__ __launch_bounds__(NW * 64) void skinny_persist_kernel(
+    const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
+    const uint16_t* __restrict__ S, const uint16_t* __restrict__ Bi, void* __restrict__ Y,
+    uint32_t M, uint32_t N, uint32_t K, int out_bf16) {
+    using C = Sk<MODE, MT, NT, G, NBW>;
+    static_assert(MODE == Q4X || MODE == Q8X, "exact modes only");
+    static_assert(C::WL == 1, "one 16-byte weight load per n-tile and block");
+    static_assert(NBW <= 4, "x of at most 4 blocks per wave stays in registers");
+    constexpr int NF = C::STEPS / C::SPF;  // quantisation groups per block
+    __shared__ __attribute__((aligned(1024))) float red[NW * C::TOT];
+
+    const uint32_t t = threadIdx.x, lane = t & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t j = lane & 15u, c = lane >> 4;
+    const uint32_t nblk = K / C::KB;
+    const uint32_t b0 = wave * nblk / NW, b1 = (wave + 1) * nblk / NW;
+    const uint32_t nb = b1 - b0;
+    const uint32_t ng = K / G;
+    const uint32_t ntiles = (N + C::NB - 1) / C::NB;
+    const size_t rb = (MODE == Q4X) ? K / 2 : K;  // weight bytes per row
+    auto blk_of = [&](int i) { return min(b0 + (uint32_t)i, nblk - 1u); };
+
+    // x: every block of this wave, once
+    u32x4_t xr[NBW][MT][C::STEPS];
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) {
+        const uint32_t k0 = blk_of(i) * C::KB;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const uint16_t* xrow = X + (size_t)min(mt * 16u + j, M - 1u) * K;
+#pragma unroll
+            for (int r = 0; r < C::STEPS; ++r)
+                xr[i][mt][r] = *reinterpret_cast<const u32x4_t*>(xrow + k0 + kmap<MODE, G>(c, r));
+        }
+    }
+
+    // block i of tile tt: this lane's 16 weight bytes per n-tile and its
+    // row's scale / bias of each of the block's groups
+    u32x4_t wr[NBW][NT];
+    uint32_t sv[NBW][NT][NF], bv[NBW][NT][NF];
+    auto load_block = [&](uint32_t tt, int i) {
+        const uint32_t blk = blk_of(i), k0 = blk * C::KB;
+        const uint32_t byte = (MODE == Q8X) ? k0 + 16u * c : k0 / 2 + 16u * c;
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+            const uint32_t n = min(tt * C::NB + nt * 16u + j, N - 1u);
+            wr[i][nt] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4_t*>(W + (size_t)n * rb + byte));
+#pragma unroll
+            for (int f = 0; f < NF; ++f) {
+                const uint32_t g = (k0 + f * C::SPF * 32u) / G;
+                sv[i][nt][f] = S[(size_t)n * ng + g];
+                bv[i][nt][f] = Bi[(size_t)n * ng + g];
+            }
+        }
+    };
+
+    const bf16x8_t ones = as_bf16x8_u(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+    const NibConst nk = nib_const();
+    const bool bf = out_bf16 != 0;
+
+    uint32_t tile = blockIdx.x;
+#pragma unroll
+    for (int i = 0; i < NBW; ++i) load_block(tile, i);
+
+    for (;;) {
+        const uint32_t nxt = tile + gridDim.x;
+        const bool more = nxt < ntiles;
+        const uint32_t n0 = tile * C::NB;
+        f32x4_t acc[NT][MT];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+        for (int i = 0; i < NBW; ++i) {
+            const bool valid = (uint32_t)i < nb;
+            bf16x8_t xf[MT][C::STEPS];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int r = 0; r < C::STEPS; ++r) xf[mt][r] = x_frag<MODE>(xr[i][mt][r]);
+            f32x4_t dx[NF][MT];
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    dx[f][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int r = f * C::SPF; r < (f + 1) * C::SPF; ++r)
+                        dx[f][mt] = mfma16(xf[mt][r], ones, dx[f][mt]);
+                }
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt) {
+                uint32_t w0 = wr[i][nt][0], w1 = wr[i][nt][1];
+                uint32_t w2 = wr[i][nt][2], w3 = wr[i][nt][3];
+                if constexpr (MODE == Q8X || G == 64 || G == 32) {
+                    swap32u(w0, w2);
+                    swap32u(w1, w3);
+                }
+                if constexpr (MODE == Q4X && G == 32) {
+                    swap16u(w0, w1);
+                    swap16u(w2, w3);
+                }
+                const uint32_t wv[4] = {w0, w1, w2, w3};
+#pragma unroll
+                for (int f = 0; f < NF; ++f) {
+                    f32x4_t dd[MT], dh[MT];
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        dd[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                        dh[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                    }
+#pragma unroll
+                    for (int r = f * C::SPF; r < (f + 1) * C::SPF; ++r) {
+                        if constexpr (MODE == Q4X) {
+                            const uint32_t v = wv[r];
+                            const bf16x8_t bfr = as_bf16x8_u(nib2(v, nk), nib2(v >> 4, nk),
+                                                             nib2(v >> 8, nk), nib2(v >> 12, nk));
+#pragma unroll
+                            for (int mt = 0; mt < MT; ++mt) dd[mt] = mfma16(xf[mt][r], bfr, dd[mt]);
+                        } else {
+                            const uint32_t vx = wv[2 * r], vy = wv[2 * r + 1];
+                            const bf16x8_t blo = as_bf16x8_u(nib2(vx, nk), nib2(vx >> 8, nk),
+                                                             nib2(vy, nk), nib2(vy >> 8, nk));
+                            const bf16x8_t bhi = as_bf16x8_u(nib2(vx >> 4, nk), nib2(vx >> 12, nk),
+                                                             nib2(vy >> 4, nk), nib2(vy >> 12, nk));
+#pragma unroll
+                            for (int mt = 0; mt < MT; ++mt) {
+                                dd[mt] = mfma16(xf[mt][r], blo, dd[mt]);
+                                dh[mt] = mfma16(xf[mt][r], bhi, dh[mt]);
+                            }
+                        }
+                    }
+                    const float sc = valid ? bf16_bits_to_f32(sv[i][nt][f]) : 0.f;
+                    const float bi = valid ? bf16_bits_to_f32(bv[i][nt][f]) : 0.f;
+                    const float bx = (MODE == Q4X) ? fmaf(-128.f, sc, bi) : fmaf(-2176.f, sc, bi);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float v = (MODE == Q4X) ? dd[mt][e] : fmaf(16.f, dh[mt][e], dd[mt][e]);
+                            acc[nt][mt][e] = fmaf(sc, v, fmaf(bx, dx[f][mt][e], acc[nt][mt][e]));
+                        }
+                }
+            }
+            // this block's registers are free again: the next tile's block i
+            if (more) load_block(nxt, i);
+        }
+
+        // cross-wave reduction in fixed wave order, then the store
+        __syncthreads();
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    red[wave * C::TOT + ((nt * MT + mt) * 4 + e) * 64 + lane] = acc[nt][mt][e];
+        __syncthreads();
+        for (uint32_t e = t; e < (uint32_t)C::TOT; e += NW * 64) {
+            float v = red[e];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) v += red[w * C::TOT + e];
+            const uint32_t ln = e & 63u, e4 = (e >> 6) & 3u, tm = e >> 8;
+            const uint32_t nt = tm / MT, mt = tm % MT;
+            const uint32_t n = n0 + nt * 16u + (ln & 15u);
+            const uint32_t m = mt * 16u + 4u * (ln >> 4) + e4;
+            if (n < N && m < M) store_out(Y, (size_t)m * N + n, v, bf);
+        }
+        if (!more) break;
+        tile = nxt;
+        // the next tile's reduction writes red: every wave has read it
+        __syncthreads();
+    }
+}
+
+// Workgroups of the persistent kernel: as many as are resident at once on
+// the device (CUs x occupancy), at most one per row tile.
+template <int MODE, int MT, int NT, int G, int NBW>
+hipError_t launch_persist(const void* X, const void* W, const void* S, const void* B, void* Y,
+                          uint32_t M, uint32_t N, uint32_t K, int out_bf16, hipStream_t st) {
+    auto kern = skinny_persist_kernel<MODE, MT, NT, G, NBW>;
+    int dev = 0, ncu = 0, occ = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, NW * 64, 0);
+    if (e != hipSuccess) return e;
+    const uint32_t ntiles = (N + 16 * NT - 1) / (16 * NT);
+    const uint32_t grid = std::min<uint32_t>(ntiles, (uint32_t)std::max(1, ncu * std::max(1, occ)));
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), 0, st, (const uint16_t*)X,
+                       (const uint8_t*)W, (const uint16_t*)S, (const uint16_t*)B, Y, M, N, K,
+                       out_bf16);
+    return hipGetLastError();
+}
+
 template <int MODE, int MT, int NT, int G, int NBW>
 hipError_t launch_sk(const void* X, const void* W, const void* S, const void* B, void* Y,
                      uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t SK,
                      hipStream_t st) {
     const uint32_t nwg = (N + 16 * NT - 1) / (16 * NT);
+    // persistent row-tile loop for vocabulary-sized N (see skinny_persist_kernel)
+    if constexpr (persist_fits(MODE, MT, NT, G, NBW)) {
+        bool persist = SK == 1 && nwg >= 1024 && MT >= 2;
+        if (const char* e = getenv("MIORI_SKINNY_PERSIST")) persist = SK == 1 && atoi(e) != 0;
+        if (persist) return launch_persist<MODE, MT, NT, G, NBW>(X, W, S, B, Y, M, N, K, out_bf16, st);
+    }
     float* part = nullptr;
     if (SK > 1) {
         const hipError_t e = workspace_get(st, (size_t)SK * M * N * 4, &part);
@@ -552,6 +781,23 @@ hipError_t by_shape(uint32_t G, const void* X, const void* W, const void* S, con
     // (a function of N and K only, so the fused 4-bit and the bf16 products
     // of one shape split alike and stay bit-identical)
     while (sk > 1 && (K / kb) % sk != 0) --sk;
+    // vocabulary-sized N, exact modes: the persistent kernel (x read once per
+    // workgroup, next tile's loads in flight) with the widest n-tile count
+    // whose registers fit (an element's k order does not depend on NT)
+    // (measured slower at M <= 16: 8-bit lm_head M=8 79 -> 111 us)
+    const char* pe = getenv("MIORI_SKINNY_PERSIST");
+    const bool persist_ok = pe ? atoi(pe) != 0 : M > 16;
+    if ((MODE == Q4X || MODE == Q8X) && sk == 1 && N >= 32768 && persist_ok &&
+        !getenv("MIORI_SKINNY_NT")) {
+        const int mt = M <= 16 ? 1 : 2;
+        const int nbw = nbw_of(K, kb);
+        for (int cand : {4, 2, 1}) {
+            if (cand <= nt && persist_fits(MODE, mt, cand, (int)G, nbw)) {
+                nt = cand;
+                break;
+            }
+        }
+    }
     if (M <= 16) return by_nt<MODE, 1>(nt, G, X, W, S, B, Y, M, N, K, out_bf16, sk, st);
     return by_nt<MODE, 2>(nt, G, X, W, S, B, Y, M, N, K, out_bf16, sk, st);
 }
