@@ -583,7 +583,7 @@ hipError_t launch_tile(const void* A, const void* B, const void* q, const void* 
 // (SK*MN*4 bytes written and read back at ~5 TB/s, MN the padded output
 // size). A function of the tile grid and K only, so the fused and the
 // two-step products of one shape take the same path.
-uint32_t pick_split(uint32_t tiles, uint32_t KT, uint64_t MN) {
+uint32_t pick_split(uint32_t tiles, uint32_t KT, uint64_t MN, uint64_t* cost_out = nullptr) {
     uint32_t best = 1;
     uint64_t best_cost = 2ull * ((tiles + 255) / 256) * KT;
     for (uint32_t sk = 2; sk <= 16 && KT / sk >= 4; ++sk) {
@@ -592,7 +592,22 @@ uint32_t pick_split(uint32_t tiles, uint32_t KT, uint64_t MN) {
         const uint64_t cost = 2 * rounds * ((KT + sk - 1) / sk) + 10 + traffic;
         if (cost < best_cost) { best = sk; best_cost = cost; }
     }
+    if (cost_out) *cost_out = best_cost;
     return best;
+}
+
+// 256x128 or 128x128 tiles: the cheaper by the split-K cost model (each on
+// its padded grid, with its best split), a 256x128 round weighted 1.35x a
+// 128x128 one (fused 4-bit: 56 us per 256x128 round at M=1024, N=8192, K=2048;
+// 37 us per 128x128 round at M=1472). A function of the tile grids and K
+// only, so the fused and the bf16 products of one shape pick alike.
+int pick_tile_256x128(uint32_t M, uint32_t N, uint32_t K) {
+    const uint32_t t0 = ((M + 255) / 256) * ((N + 127) / 128);
+    const uint32_t t1 = ((M + 127) / 128) * ((N + 127) / 128);
+    uint64_t c0 = 0, c1 = 0;
+    pick_split(t0, K / 64, (uint64_t)t0 * 256 * 128, &c0);
+    pick_split(t1, K / 64, (uint64_t)t1 * 128 * 128, &c1);
+    return c0 * 27 <= c1 * 20 ? 0 : 1;
 }
 
 }  // namespace
@@ -611,18 +626,19 @@ hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* 
     //    fused and bf16 products stay bit-identical. Measured against
     //    128x128 tiles with split partials: bf16 M=1024 N=2048 19.7 -> 15.0
     //    us, M=256 N=8192 19.9 -> 15.3 us; fused M=1024 N=512 25.8 -> 16.7.
-    //  * otherwise 256x128 tiles when they come in whole waves of 256 (one
-    //    per CU), else 128x128 tiles with K split over workgroups to fill
-    //    the chip.
+    //  * otherwise 256x128 or 128x128 tiles, whichever the split-K cost
+    //    model rates cheaper (pick_tile_256x128). Against the earlier rule
+    //    (256x128 only in whole waves of 256): fused M=1472 N=8192 K=2048
+    //    110 -> 101 us, M=1024 K=8192 N=2048 78.8 -> 67.3 us; bf16 M=1472
+    //    K=8192 N=2048 92 -> 85 us.
     const uint64_t huge = (uint64_t)((M + 255) / 256) * ((N + 255) / 256);
-    const uint64_t big = (uint64_t)((M + 255) / 256) * ((N + 127) / 128);
     const uint64_t t64 = (uint64_t)((M + 63) / 64) * ((N + 63) / 64);
-    int tile = (big >= 256 && big % 256 == 0) ? 0 : 1;
+    int tile = pick_tile_256x128(M, N, K);
     if (!q && huge >= 192) tile = 2;
     else if (K <= 4096 && t64 <= 512) tile = q ? 3 : 4;
     if (const char* e = getenv("MIORI_GEMM_TILE")) tile = atoi(e);
     if (tile == 2 && !q) return launch_cfg<256, 256, false, 64>(A, B, q, s, b, C, M, N, K, out_bf16, 1, st);
-    if (tile == 2) tile = (big >= 256 && big % 256 == 0) ? 0 : 1;  // fused: no 256x256 variant
+    if (tile == 2) tile = pick_tile_256x128(M, N, K);  // fused: no 256x256 variant
     // (64x64 splits as the 64x128 grid, the fused path's tile)
     const uint32_t tbm = tile == 0 ? 256 : (tile == 3 || tile == 4) ? 64 : 128;
     const uint32_t tbn = 128;
