@@ -38,7 +38,6 @@
 
 #include <stdlib.h>
 
-#include <algorithm>
 #include <type_traits>
 
 namespace miori {
@@ -46,12 +45,12 @@ namespace miori {
 namespace {
 
 enum { Q4X = 0, Q8X = 1, Q4F = 2, BF16 = 3 };
-constexpr int NW = 8;  // waves per workgroup
+constexpr int NW = 8;  // waves per workgroup (widest form; exact modes also use 4)
 
 template <int N>
 using ic = std::integral_constant<int, N>;
 
-template <int MODE, int MT, int NT, int G, int NBW>
+template <int MODE, int MT, int NT, int G, int NBW, int NWV>
 struct Sk {
     static constexpr bool EXACT = MODE == Q4X || MODE == Q8X;
     static constexpr int KB = MODE == Q8X ? 64 : 128;          // k per block
@@ -66,14 +65,14 @@ struct Sk {
     static constexpr int TOT = NT * MT * 4 * 64;                  // partial floats per wave
     static constexpr int L = NT * WL + MT * STEPS;                // loads per block
     // scale / bias tiles of the workgroup's rows in LDS (all K/G groups of up
-    // to NBW * NW blocks), rounded up to whole 1 KiB DMA chunks
+    // to NBW * NWV blocks), rounded up to whole 1 KiB DMA chunks
     static constexpr int NB = 16 * NT;
     // (all K / G groups of a row: sized for the largest supported K, 8 blocks
     // per wave, so a workgroup of a K split indexes groups absolutely)
-    static constexpr int NGMAX = EXACT || MODE == Q4F ? (8 * NW * KB) / G : 0;
+    static constexpr int NGMAX = EXACT || MODE == Q4F ? (8 * NWV * KB) / G : 0;
     // (+ room for the masked reads of padding blocks past a row's end)
     static constexpr int SB_BYTES = ((NB * NGMAX * 2 + NBW * KB / 16 + 1023) / 1024) * 1024;
-    static constexpr int RED_BYTES = NW * TOT * 4;
+    static constexpr int RED_BYTES = NWV * TOT * 4;
     static constexpr int LDS = 2 * SB_BYTES > RED_BYTES ? 2 * SB_BYTES : RED_BYTES;
     static constexpr int DEPTH = PD < NBW ? PD : NBW;             // slots actually used
     static_assert((DEPTH - 1) * L < 64, "vmcnt range");
@@ -171,12 +170,12 @@ __device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-template <int MODE, int MT, int NT, int G, int NBW>
-__global__ __launch_bounds__(NW * 64) void skinny_kernel(
+template <int MODE, int MT, int NT, int G, int NBW, int NWV>
+__global__ __launch_bounds__(NWV * 64) void skinny_kernel(
     const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
     const uint16_t* __restrict__ S, const uint16_t* __restrict__ Bi, void* __restrict__ Y,
     uint32_t M, uint32_t N, uint32_t K, int out_bf16, float* __restrict__ part) {
-    using C = Sk<MODE, MT, NT, G, NBW>;
+    using C = Sk<MODE, MT, NT, G, NBW, NWV>;
     // scale / bias tiles first, the cross-wave reduction buffer at the end
     __shared__ __attribute__((aligned(1024))) uint8_t lds[C::LDS];
     float* red = reinterpret_cast<float*>(lds);
@@ -192,7 +191,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
     const uint32_t nblk = K / C::KB;
     // this workgroup's K blocks: [kb0, kb0 + nloc) (split gridDim.y ways)
     const uint32_t nloc = nblk / gridDim.y, kb0 = blockIdx.y * nloc;
-    const uint32_t b0 = kb0 + wave * nloc / NW, b1 = kb0 + (wave + 1) * nloc / NW;
+    const uint32_t b0 = kb0 + wave * nloc / NWV, b1 = kb0 + (wave + 1) * nloc / NWV;
     const uint32_t nb = b1 - b0;
     const uint32_t ng = (MODE == BF16) ? 1u : K / G;
 
@@ -416,7 +415,7 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
         const uint32_t tb = C::NB * ng * 2u;                 // tile bytes
         const size_t total = (size_t)N * ng * 2u;            // array bytes
         const size_t base = (size_t)n0 * ng * 2u;
-        for (uint32_t q = wave; q * 1024u < tb; q += NW) {
+        for (uint32_t q = wave; q * 1024u < tb; q += NWV) {
             const size_t off = min(base + q * 1024u + lane * 16u, total - 16u);
             dma16(reinterpret_cast<const uint8_t*>(S) + off, lds + q * 1024u);
             dma16(reinterpret_cast<const uint8_t*>(Bi) + off, lds + C::SB_BYTES + q * 1024u);
@@ -441,10 +440,10 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
             for (int e = 0; e < 4; ++e) red[wave * C::TOT + ((nt * MT + mt) * 4 + e) * 64 + lane] = acc[nt][mt][e];
     __syncthreads();
     const bool bf = out_bf16 != 0;
-    for (uint32_t e = t; e < (uint32_t)C::TOT; e += NW * 64) {
+    for (uint32_t e = t; e < (uint32_t)C::TOT; e += NWV * 64) {
         float v = red[e];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) v += red[w * C::TOT + e];
+        for (int w = 1; w < NWV; ++w) v += red[w * C::TOT + e];
         const uint32_t ln = e & 63u, e4 = (e >> 6) & 3u, tm = e >> 8;
         const uint32_t nt = tm / MT, mt = tm % MT;
         const uint32_t n = n0 + nt * 16u + (ln & 15u);
@@ -458,246 +457,20 @@ __global__ __launch_bounds__(NW * 64) void skinny_kernel(
     }
 }
 
-// Register budget of the persistent kernel: x of all NBW blocks, one weight
-// slot per block and the accumulators stay live across the tile loop (in
-// 4-byte registers; G = 32's extra word exchange costs more). Instances over
-// the bound were measured to spill.
-constexpr bool persist_fits(int mode, int mt, int nt, int g, int nbw) {
-    const int steps = mode == Q8X ? 2 : 4;
-    return (mode == Q4X || mode == Q8X) && nbw <= 4 &&
-           nbw * mt * steps * 4 + nbw * nt * 4 + nt * mt * 4 + (g == 32 ? 48 : 0) <= 88;
-}
-
-// Persistent variant for vocabulary-sized N (exact modes Q4X / Q8X, no K
-// split): each workgroup loops over row tiles t = blockIdx.x, + gridDim.x,
-// ... . Per tile it computes what skinny_kernel computes for one workgroup
-// (the same blocks per wave, per-element k order and wave reduction, so the
-// results are identical), with two differences:
-//  * x (this wave's NBW K blocks) is loaded into registers once, not once per
-//    tile: at M = 32, K = 2048 that is 128 KB per workgroup saved per tile;
-//  * after block i of tile t is computed, the weights, scales and biases of
-//    block i of the next tile are loaded into the same registers, so the
-//    next tile's loads are in flight while this tile finishes, is reduced
-//    and is stored.
-// Every load here is compiler code (no inline-asm loads, no hand-placed
-// waits): the loads the loop carries into its next iteration are waited for
-// by the compiler wherever their registers are used or copied.
-template <int MODE, int MT, int NT, int G, int NBW>
-__global__ __launch_bounds__(NW * 64) void skinny_persist_kernel(
-    const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
-    const uint16_t* __restrict__ S, const uint16_t* __restrict__ Bi, void* __restrict__ Y,
-    uint32_t M, uint32_t N, uint32_t K, int out_bf16) {
-    using C = Sk<MODE, MT, NT, G, NBW>;
-    static_assert(MODE == Q4X || MODE == Q8X, "exact modes only");
-    static_assert(C::WL == 1, "one 16-byte weight load per n-tile and block");
-    static_assert(NBW <= 4, "x of at most 4 blocks per wave stays in registers");
-    constexpr int NF = C::STEPS / C::SPF;  // quantisation groups per block
-    __shared__ __attribute__((aligned(1024))) float red[NW * C::TOT];
-
-    const uint32_t t = threadIdx.x, lane = t & 63u;
-    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const uint32_t j = lane & 15u, c = lane >> 4;
-    const uint32_t nblk = K / C::KB;
-    const uint32_t b0 = wave * nblk / NW, b1 = (wave + 1) * nblk / NW;
-    const uint32_t nb = b1 - b0;
-    const uint32_t ng = K / G;
-    const uint32_t ntiles = (N + C::NB - 1) / C::NB;
-    const size_t rb = (MODE == Q4X) ? K / 2 : K;  // weight bytes per row
-    auto blk_of = [&](int i) { return min(b0 + (uint32_t)i, nblk - 1u); };
-
-    // x: every block of this wave, once
-    u32x4_t xr[NBW][MT][C::STEPS];
-#pragma unroll
-    for (int i = 0; i < NBW; ++i) {
-        const uint32_t k0 = blk_of(i) * C::KB;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const uint16_t* xrow = X + (size_t)min(mt * 16u + j, M - 1u) * K;
-#pragma unroll
-            for (int r = 0; r < C::STEPS; ++r)
-                xr[i][mt][r] = *reinterpret_cast<const u32x4_t*>(xrow + k0 + kmap<MODE, G>(c, r));
-        }
-    }
-
-    // block i of tile tt: this lane's 16 weight bytes per n-tile and its
-    // row's scale / bias of each of the block's groups
-    u32x4_t wr[NBW][NT];
-    uint32_t sv[NBW][NT][NF], bv[NBW][NT][NF];
-    auto load_block = [&](uint32_t tt, int i) {
-        const uint32_t blk = blk_of(i), k0 = blk * C::KB;
-        const uint32_t byte = (MODE == Q8X) ? k0 + 16u * c : k0 / 2 + 16u * c;
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-            const uint32_t n = min(tt * C::NB + nt * 16u + j, N - 1u);
-            wr[i][nt] = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x4_t*>(W + (size_t)n * rb + byte));
-#pragma unroll
-            for (int f = 0; f < NF; ++f) {
-                const uint32_t g = (k0 + f * C::SPF * 32u) / G;
-                sv[i][nt][f] = S[(size_t)n * ng + g];
-                bv[i][nt][f] = Bi[(size_t)n * ng + g];
-            }
-        }
-    };
-
-    const bf16x8_t ones = as_bf16x8_u(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
-    const NibConst nk = nib_const();
-    const bool bf = out_bf16 != 0;
-
-    uint32_t tile = blockIdx.x;
-#pragma unroll
-    for (int i = 0; i < NBW; ++i) load_block(tile, i);
-
-    for (;;) {
-        const uint32_t nxt = tile + gridDim.x;
-        const bool more = nxt < ntiles;
-        const uint32_t n0 = tile * C::NB;
-        f32x4_t acc[NT][MT];
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-#pragma unroll
-        for (int i = 0; i < NBW; ++i) {
-            const bool valid = (uint32_t)i < nb;
-            bf16x8_t xf[MT][C::STEPS];
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int r = 0; r < C::STEPS; ++r) xf[mt][r] = x_frag<MODE>(xr[i][mt][r]);
-            f32x4_t dx[NF][MT];
-#pragma unroll
-            for (int f = 0; f < NF; ++f)
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) {
-                    dx[f][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int r = f * C::SPF; r < (f + 1) * C::SPF; ++r)
-                        dx[f][mt] = mfma16(xf[mt][r], ones, dx[f][mt]);
-                }
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-                uint32_t w0 = wr[i][nt][0], w1 = wr[i][nt][1];
-                uint32_t w2 = wr[i][nt][2], w3 = wr[i][nt][3];
-                if constexpr (MODE == Q8X || G == 64 || G == 32) {
-                    swap32u(w0, w2);
-                    swap32u(w1, w3);
-                }
-                if constexpr (MODE == Q4X && G == 32) {
-                    swap16u(w0, w1);
-                    swap16u(w2, w3);
-                }
-                const uint32_t wv[4] = {w0, w1, w2, w3};
-#pragma unroll
-                for (int f = 0; f < NF; ++f) {
-                    f32x4_t dd[MT], dh[MT];
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) {
-                        dd[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-                        dh[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-                    }
-#pragma unroll
-                    for (int r = f * C::SPF; r < (f + 1) * C::SPF; ++r) {
-                        if constexpr (MODE == Q4X) {
-                            const uint32_t v = wv[r];
-                            const bf16x8_t bfr = as_bf16x8_u(nib2(v, nk), nib2(v >> 4, nk),
-                                                             nib2(v >> 8, nk), nib2(v >> 12, nk));
-#pragma unroll
-                            for (int mt = 0; mt < MT; ++mt) dd[mt] = mfma16(xf[mt][r], bfr, dd[mt]);
-                        } else {
-                            const uint32_t vx = wv[2 * r], vy = wv[2 * r + 1];
-                            const bf16x8_t blo = as_bf16x8_u(nib2(vx, nk), nib2(vx >> 8, nk),
-                                                             nib2(vy, nk), nib2(vy >> 8, nk));
-                            const bf16x8_t bhi = as_bf16x8_u(nib2(vx >> 4, nk), nib2(vx >> 12, nk),
-                                                             nib2(vy >> 4, nk), nib2(vy >> 12, nk));
-#pragma unroll
-                            for (int mt = 0; mt < MT; ++mt) {
-                                dd[mt] = mfma16(xf[mt][r], blo, dd[mt]);
-                                dh[mt] = mfma16(xf[mt][r], bhi, dh[mt]);
-                            }
-                        }
-                    }
-                    const float sc = valid ? bf16_bits_to_f32(sv[i][nt][f]) : 0.f;
-                    const float bi = valid ? bf16_bits_to_f32(bv[i][nt][f]) : 0.f;
-                    const float bx = (MODE == Q4X) ? fmaf(-128.f, sc, bi) : fmaf(-2176.f, sc, bi);
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const float v = (MODE == Q4X) ? dd[mt][e] : fmaf(16.f, dh[mt][e], dd[mt][e]);
-                            acc[nt][mt][e] = fmaf(sc, v, fmaf(bx, dx[f][mt][e], acc[nt][mt][e]));
-                        }
-                }
-            }
-            // this block's registers are free again: the next tile's block i
-            if (more) load_block(nxt, i);
-        }
-
-        // cross-wave reduction in fixed wave order, then the store
-        __syncthreads();
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    red[wave * C::TOT + ((nt * MT + mt) * 4 + e) * 64 + lane] = acc[nt][mt][e];
-        __syncthreads();
-        for (uint32_t e = t; e < (uint32_t)C::TOT; e += NW * 64) {
-            float v = red[e];
-#pragma unroll
-            for (int w = 1; w < NW; ++w) v += red[w * C::TOT + e];
-            const uint32_t ln = e & 63u, e4 = (e >> 6) & 3u, tm = e >> 8;
-            const uint32_t nt = tm / MT, mt = tm % MT;
-            const uint32_t n = n0 + nt * 16u + (ln & 15u);
-            const uint32_t m = mt * 16u + 4u * (ln >> 4) + e4;
-            if (n < N && m < M) store_out(Y, (size_t)m * N + n, v, bf);
-        }
-        if (!more) break;
-        tile = nxt;
-        // the next tile's reduction writes red: every wave has read it
-        __syncthreads();
-    }
-}
-
-// Workgroups of the persistent kernel: as many as are resident at once on
-// the device (CUs x occupancy), at most one per row tile.
-template <int MODE, int MT, int NT, int G, int NBW>
-hipError_t launch_persist(const void* X, const void* W, const void* S, const void* B, void* Y,
-                          uint32_t M, uint32_t N, uint32_t K, int out_bf16, hipStream_t st) {
-    auto kern = skinny_persist_kernel<MODE, MT, NT, G, NBW>;
-    int dev = 0, ncu = 0, occ = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e == hipSuccess) e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, NW * 64, 0);
-    if (e != hipSuccess) return e;
-    const uint32_t ntiles = (N + 16 * NT - 1) / (16 * NT);
-    const uint32_t grid = std::min<uint32_t>(ntiles, (uint32_t)std::max(1, ncu * std::max(1, occ)));
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(NW * 64), 0, st, (const uint16_t*)X,
-                       (const uint8_t*)W, (const uint16_t*)S, (const uint16_t*)B, Y, M, N, K,
-                       out_bf16);
-    return hipGetLastError();
-}
-
-template <int MODE, int MT, int NT, int G, int NBW>
+template <int MODE, int MT, int NT, int G, int NBW, int NWV>
 hipError_t launch_sk(const void* X, const void* W, const void* S, const void* B, void* Y,
                      uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t SK,
                      hipStream_t st) {
+    // (the kernel's scale / bias LDS tiles hold 8 blocks per wave)
+    if (K / SK / (MODE == Q8X ? 64u : 128u) > 8u * NWV) return hipErrorInvalidValue;
     const uint32_t nwg = (N + 16 * NT - 1) / (16 * NT);
-    // persistent row-tile loop for vocabulary-sized N (see skinny_persist_kernel)
-    if constexpr (persist_fits(MODE, MT, NT, G, NBW)) {
-        bool persist = SK == 1 && nwg >= 1024 && MT >= 2;
-        if (const char* e = getenv("MIORI_SKINNY_PERSIST")) persist = SK == 1 && atoi(e) != 0;
-        if (persist) return launch_persist<MODE, MT, NT, G, NBW>(X, W, S, B, Y, M, N, K, out_bf16, st);
-    }
     float* part = nullptr;
     if (SK > 1) {
         const hipError_t e = workspace_get(st, (size_t)SK * M * N * 4, &part);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((skinny_kernel<MODE, MT, NT, G, NBW>), dim3(nwg, SK), dim3(NW * 64), 0, st,
-                       (const uint16_t*)X, (const uint8_t*)W, (const uint16_t*)S,
+    hipLaunchKernelGGL((skinny_kernel<MODE, MT, NT, G, NBW, NWV>), dim3(nwg, SK), dim3(NWV * 64),
+                       0, st, (const uint16_t*)X, (const uint8_t*)W, (const uint16_t*)S,
                        (const uint16_t*)B, Y, M, N, K, out_bf16, part);
     if (SK > 1) {
         const hipError_t e = hipGetLastError();
@@ -708,33 +481,33 @@ hipError_t launch_sk(const void* X, const void* W, const void* S, const void* B,
 }
 
 // blocks per wave, rounded up to 1, 2, 4 or 8
-inline int nbw_of(uint32_t K, uint32_t kb) {
-    const uint32_t per = (K / kb + NW - 1) / NW;
+inline int nbw_of(uint32_t K, uint32_t kb, int nw = NW) {
+    const uint32_t per = (K / kb + nw - 1) / nw;
     return per <= 1 ? 1 : per <= 2 ? 2 : per <= 4 ? 4 : 8;
 }
 
-template <int MODE, int MT, int NT, int G>
+template <int MODE, int MT, int NT, int G, int NWV>
 hipError_t by_nbw(const void* X, const void* W, const void* S, const void* B, void* Y,
                   uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t SK, hipStream_t st) {
-    switch (nbw_of(K / SK, MODE == Q8X ? 64u : 128u)) {
-        case 1: return launch_sk<MODE, MT, NT, G, 1>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
-        case 2: return launch_sk<MODE, MT, NT, G, 2>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
-        case 4: return launch_sk<MODE, MT, NT, G, 4>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
+    switch (nbw_of(K / SK, MODE == Q8X ? 64u : 128u, NWV)) {
+        case 1: return launch_sk<MODE, MT, NT, G, 1, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
+        case 2: return launch_sk<MODE, MT, NT, G, 2, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
+        case 4: return launch_sk<MODE, MT, NT, G, 4, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
     }
-    return launch_sk<MODE, MT, NT, G, 8>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
+    return launch_sk<MODE, MT, NT, G, 8, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
 }
 
-template <int MODE, int MT, int NT>
+template <int MODE, int MT, int NT, int NWV = NW>
 hipError_t by_group(uint32_t G, const void* X, const void* W, const void* S, const void* B,
                     void* Y, uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t SK,
                     hipStream_t st) {
     if constexpr (MODE == BF16) {
-        return by_nbw<BF16, MT, NT, 64>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
+        return by_nbw<BF16, MT, NT, 64, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
     } else {
         switch (G) {
-            case 32: return by_nbw<MODE, MT, NT, 32>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
-            case 64: return by_nbw<MODE, MT, NT, 64>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
-            case 128: return by_nbw<MODE, MT, NT, 128>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
+            case 32: return by_nbw<MODE, MT, NT, 32, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
+            case 64: return by_nbw<MODE, MT, NT, 64, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
+            case 128: return by_nbw<MODE, MT, NT, 128, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
         }
         return hipErrorInvalidValue;
     }
@@ -781,21 +554,23 @@ hipError_t by_shape(uint32_t G, const void* X, const void* W, const void* S, con
     // (a function of N and K only, so the fused 4-bit and the bf16 products
     // of one shape split alike and stay bit-identical)
     while (sk > 1 && (K / kb) % sk != 0) --sk;
-    // vocabulary-sized N, exact modes: the persistent kernel (x read once per
-    // workgroup, next tile's loads in flight) with the widest n-tile count
-    // whose registers fit (an element's k order does not depend on NT)
-    // (measured slower at M <= 16: 8-bit lm_head M=8 79 -> 111 us)
-    const char* pe = getenv("MIORI_SKINNY_PERSIST");
-    const bool persist_ok = pe ? atoi(pe) != 0 : M > 16;
-    if ((MODE == Q4X || MODE == Q8X) && sk == 1 && N >= 32768 && persist_ok &&
-        !getenv("MIORI_SKINNY_NT")) {
-        const int mt = M <= 16 ? 1 : 2;
-        const int nbw = nbw_of(K, kb);
-        for (int cand : {4, 2, 1}) {
-            if (cand <= nt && persist_fits(MODE, mt, cand, (int)G, nbw)) {
-                nt = cand;
-                break;
-            }
+    // Vocabulary-sized N, exact modes: workgroups of four waves, with four
+    // n-tiles above M = 8 and two up to it. Each wave streams twice the K
+    // blocks of the eight-wave form, and x is loaded once per 64 rows.
+    // Measured (N = 131072, K = 2048, against the best eight-wave form):
+    // 8-bit M=32 140 -> 117 us, M=16 90 -> 85, M=8 80.5 -> 78.7; 4-bit at
+    // N = 65536 M=32 45.5 -> 38.5 us, M=8 25.0 -> 24.5 (four n-tiles: 26.4).
+    // Needs the whole K in 8 blocks per wave and no K split.
+    int nw = 8;
+    if ((MODE == Q4X || MODE == Q8X) && sk == 1 && N >= 32768 && K / kb <= 32 &&
+        !getenv("MIORI_SKINNY_NT"))
+        nw = 4;
+    if (const char* e = getenv("MIORI_SKINNY_NW")) nw = (atoi(e) == 4 && sk == 1 && K / kb <= 32) ? 4 : 8;
+    if constexpr (MODE == Q4X || MODE == Q8X) {
+        if (nw == 4) {
+            if (M <= 8) return by_group<MODE, 1, 2, 4>(G, X, W, S, B, Y, M, N, K, out_bf16, sk, st);
+            if (M <= 16) return by_group<MODE, 1, 4, 4>(G, X, W, S, B, Y, M, N, K, out_bf16, sk, st);
+            return by_group<MODE, 2, 4, 4>(G, X, W, S, B, Y, M, N, K, out_bf16, sk, st);
         }
     }
     if (M <= 16) return by_nt<MODE, 1>(nt, G, X, W, S, B, Y, M, N, K, out_bf16, sk, st);

@@ -88,14 +88,15 @@ def test_skinny_kernel_waits(tmp_path):
     text = out.read_text()
     res = check_file(text, "skinny_kernel")
     assert len(res) >= 100, "expected every skinny_kernel instantiation"
-    pers = check_file(text, "skinny_persist_kernel")
-    assert len(pers) >= 10, "expected the persistent instantiations"
-    res.update(pers)
+    # the four-wave forms of the exact modes (template arguments MODE 0/1,
+    # MT, NT = 2 or 4, G, NBW, four waves)
+    four = [k for k in res if re.search(r"skinny_kernelILi[01]ELi[12]ELi[24]ELi\d+ELi[1248]ELi4EE", k)]
+    assert len(four) >= 36, "expected the four-wave instantiations"
     bad = {k: v for k, v in res.items() if v}
     assert not bad, {k[:80]: v[:3] for k, v in bad.items()}
     # no register spills: a spill is a copy, and copying a register an inline
     # asm load is still filling reads garbage
-    names = re.findall(r"\.name:\s+(_Z\S*skinny_(?:persist_)?kernel\S*)", text)
+    names = re.findall(r"\.name:\s+(_Z\S*skinny_kernel\S*)", text)
     scratch = re.findall(r"\.name:\s+(\S+)(?:(?!\.name:).)*?\.private_segment_fixed_size:\s+(\d+)", text, re.S)
-    spilled = [n for n, sz in scratch if ("skinny_kernel" in n or "skinny_persist_kernel" in n) and int(sz) > 0]
+    spilled = [n for n, sz in scratch if "skinny_kernel" in n and int(sz) > 0]
     assert names and not spilled, spilled[:5]

@@ -178,3 +178,19 @@ def test_batched_skinny_groups(dev, bits, M, N, K, G):
     y = _run(lin, xd, M, torch.float32)
     ref = oracle.gemv_f64(w.q, w.s, w.b, x, bits, K, G, nthreads=NT)
     check_close(y, ref, f"gemv{bits}_b M={M} G={G}")
+
+
+@pytest.mark.parametrize("bits,M,N,K,G", [
+    (4, 6, 32784, 1024, 32), (4, 20, 32768, 2048, 128), (4, 32, 40000, 4096, 64),
+    (8, 5, 32800, 1024, 128), (8, 12, 32768, 2048, 32), (8, 9, 33024, 512, 64),
+])
+def test_batched_skinny_four_wave(dev, bits, M, N, K, G):
+    """Vocabulary-sized N: the four-wave workgroups (two n-tiles up to M = 8,
+    four above), every group size, ragged N and K from one to eight blocks
+    per wave."""
+    say(f"gemv{bits}_b four-wave M={M} N={N} K={K} G={G}")
+    w, lin = weights(N, K, G, bits, seed=M * 7 + G, dev=dev)
+    x, xd = acts(M, K, seed=M + 900, dev=dev)
+    y = _run(lin, xd, M, torch.bfloat16)
+    ref = oracle.gemv_f64(w.q, w.s, w.b, x, bits, K, G, nthreads=NT)
+    check_close(y, ref, f"gemv{bits}_b four-wave M={M} G={G}")
