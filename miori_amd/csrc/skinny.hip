@@ -205,8 +205,10 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
         wrow[nt] = W + (size_t)n * rb;
     }
     const uint16_t* xrow[MT];
+    // rows [m0, m0 + 16 MT) of x and y (M split over gridDim.z)
+    const uint32_t m0 = blockIdx.z * 16u * MT;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) xrow[mt] = X + (size_t)min(mt * 16u + j, M - 1u) * K;
+    for (int mt = 0; mt < MT; ++mt) xrow[mt] = X + (size_t)min(m0 + mt * 16u + j, M - 1u) * K;
 
     // block slots
     u32x4_t wr[C::DEPTH][NT][C::WL];
@@ -447,7 +449,7 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
         const uint32_t ln = e & 63u, e4 = (e >> 6) & 3u, tm = e >> 8;
         const uint32_t nt = tm / MT, mt = tm % MT;
         const uint32_t n = n0 + nt * 16u + (ln & 15u);
-        const uint32_t m = mt * 16u + 4u * (ln >> 4) + e4;
+        const uint32_t m = m0 + mt * 16u + 4u * (ln >> 4) + e4;
         if (n < N && m < M) {
             if (gridDim.y == 1)
                 store_out(Y, (size_t)m * N + n, v, bf);
@@ -460,7 +462,7 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
 template <int MODE, int MT, int NT, int G, int NBW, int NWV>
 hipError_t launch_sk(const void* X, const void* W, const void* S, const void* B, void* Y,
                      uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t SK,
-                     hipStream_t st) {
+                     hipStream_t st, uint32_t MZ = 1) {
     // (the kernel's scale / bias LDS tiles hold 8 blocks per wave)
     if (K / SK / (MODE == Q8X ? 64u : 128u) > 8u * NWV) return hipErrorInvalidValue;
     const uint32_t nwg = (N + 16 * NT - 1) / (16 * NT);
@@ -469,7 +471,7 @@ hipError_t launch_sk(const void* X, const void* W, const void* S, const void* B,
         const hipError_t e = workspace_get(st, (size_t)SK * M * N * 4, &part);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((skinny_kernel<MODE, MT, NT, G, NBW, NWV>), dim3(nwg, SK), dim3(NWV * 64),
+    hipLaunchKernelGGL((skinny_kernel<MODE, MT, NT, G, NBW, NWV>), dim3(nwg, SK, MZ), dim3(NWV * 64),
                        0, st, (const uint16_t*)X, (const uint8_t*)W, (const uint16_t*)S,
                        (const uint16_t*)B, Y, M, N, K, out_bf16, part);
     if (SK > 1) {
@@ -488,26 +490,27 @@ inline int nbw_of(uint32_t K, uint32_t kb, int nw = NW) {
 
 template <int MODE, int MT, int NT, int G, int NWV>
 hipError_t by_nbw(const void* X, const void* W, const void* S, const void* B, void* Y,
-                  uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t SK, hipStream_t st) {
+                  uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t SK, hipStream_t st,
+                  uint32_t MZ = 1) {
     switch (nbw_of(K / SK, MODE == Q8X ? 64u : 128u, NWV)) {
-        case 1: return launch_sk<MODE, MT, NT, G, 1, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
-        case 2: return launch_sk<MODE, MT, NT, G, 2, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
-        case 4: return launch_sk<MODE, MT, NT, G, 4, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
+        case 1: return launch_sk<MODE, MT, NT, G, 1, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st, MZ);
+        case 2: return launch_sk<MODE, MT, NT, G, 2, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st, MZ);
+        case 4: return launch_sk<MODE, MT, NT, G, 4, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st, MZ);
     }
-    return launch_sk<MODE, MT, NT, G, 8, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
+    return launch_sk<MODE, MT, NT, G, 8, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st, MZ);
 }
 
 template <int MODE, int MT, int NT, int NWV = NW>
 hipError_t by_group(uint32_t G, const void* X, const void* W, const void* S, const void* B,
                     void* Y, uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t SK,
-                    hipStream_t st) {
+                    hipStream_t st, uint32_t MZ = 1) {
     if constexpr (MODE == BF16) {
-        return by_nbw<BF16, MT, NT, 64, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
+        return by_nbw<BF16, MT, NT, 64, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st, MZ);
     } else {
         switch (G) {
-            case 32: return by_nbw<MODE, MT, NT, 32, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
-            case 64: return by_nbw<MODE, MT, NT, 64, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
-            case 128: return by_nbw<MODE, MT, NT, 128, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st);
+            case 32: return by_nbw<MODE, MT, NT, 32, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st, MZ);
+            case 64: return by_nbw<MODE, MT, NT, 64, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st, MZ);
+            case 128: return by_nbw<MODE, MT, NT, 128, NWV>(X, W, S, B, Y, M, N, K, out_bf16, SK, st, MZ);
         }
         return hipErrorInvalidValue;
     }
@@ -517,12 +520,12 @@ hipError_t by_group(uint32_t G, const void* X, const void* W, const void* S, con
 template <int MODE, int MT>
 hipError_t by_nt(int nt, uint32_t G, const void* X, const void* W, const void* S, const void* B,
                  void* Y, uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t SK,
-                 hipStream_t st) {
+                 hipStream_t st, uint32_t MZ = 1) {
     // (bf16 weights need 4x the load registers of a 4-bit n-tile: at most 2)
     if constexpr (MODE != BF16)
-        if (nt >= 4) return by_group<MODE, MT, 4>(G, X, W, S, B, Y, M, N, K, out_bf16, SK, st);
-    if (nt >= 2) return by_group<MODE, MT, 2>(G, X, W, S, B, Y, M, N, K, out_bf16, SK, st);
-    return by_group<MODE, MT, 1>(G, X, W, S, B, Y, M, N, K, out_bf16, SK, st);
+        if (nt >= 4) return by_group<MODE, MT, 4>(G, X, W, S, B, Y, M, N, K, out_bf16, SK, st, MZ);
+    if (nt >= 2) return by_group<MODE, MT, 2>(G, X, W, S, B, Y, M, N, K, out_bf16, SK, st, MZ);
+    return by_group<MODE, MT, 1>(G, X, W, S, B, Y, M, N, K, out_bf16, SK, st, MZ);
 }
 
 template <int MODE>
@@ -573,7 +576,19 @@ hipError_t by_shape(uint32_t G, const void* X, const void* W, const void* S, con
             return by_group<MODE, 2, 4, 4>(G, X, W, S, B, Y, M, N, K, out_bf16, sk, st);
         }
     }
-    if (M <= 16) return by_nt<MODE, 1>(nt, G, X, W, S, B, Y, M, N, K, out_bf16, sk, st);
+    // M split above M = 16 when the doubled grid still fits one round of
+    // 256 workgroups: one 16-row m-tile per workgroup (gridDim.z), the
+    // weights read once per m-tile (from L2 for the second). Every output
+    // element is computed as without the split. Measured at M = 32, K =
+    // 2048: N = 2048 7.09 -> 5.23 us (fused 7.36 -> 5.73, bf16 9.85 -> 8.04),
+    // N = 512 6.79 -> 5.12; at N = 3072 (192 -> 384 workgroups) it was
+    // slower, bf16 10.3 -> 14.2 us.
+    uint32_t mz = 1;
+    const uint32_t wgs = (N + 16u * nt - 1) / (16u * nt) * sk;
+    if (M > 16 && wgs <= 128) mz = 2;
+    if (const char* e = getenv("MIORI_SKINNY_MZ")) mz = (atoi(e) == 2 && M > 16) ? 2 : 1;
+    if (M <= 16 || mz == 2)
+        return by_nt<MODE, 1>(nt, G, X, W, S, B, Y, M, N, K, out_bf16, sk, st, mz);
     return by_nt<MODE, 2>(nt, G, X, W, S, B, Y, M, N, K, out_bf16, sk, st);
 }
 
