@@ -16,10 +16,11 @@
 // is computed. A thread reads 8 consecutive k of each of its rows as one
 // 16-byte LDS read and runs the 8 FMAs of every chain in k order. The chains
 // cannot be split over k, so the slice depth sets how many load round trips
-// a chain waits for. Three tile shapes: 64 x 64 (KT 64) for general M,
-// 16 x 128 (KT 128) for M <= 16 (the batch lm_head, where a 64-row tile would
-// waste most of its FMAs) and 16 x 16 (KT 512) for N <= 32 (gate_proj N=16);
-// element loads (any stride) use a quarter of the slice depth.
+// a chain waits for. Tile shapes: 64 x 64 (KT 64) for general M; 8 x 256
+// (KT 64), 16 x 128 (KT 128) and 32 x 128 (KT 64) for M <= 8 / 16 / 32 (the
+// batch lm_head, where a taller tile would spend half or more of its FMAs on
+// padding rows); 16 x 16 (KT 512) for N <= 32 (gate_proj N=16). Element
+// loads (any stride) use a quarter of the slice depth.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -39,9 +40,13 @@ __global__ __launch_bounds__(256) void naive_gemm_kernel(const uint16_t* __restr
     static_assert(KT % 8 == 0, "8-k chunks");
     constexpr int P = KT + 8;                     // row stride in LDS (bf16), 16-byte pad
     constexpr int CPR = KT / 8;                   // 16-byte chunks per row per slice
-    constexpr int CA = TM * CPR / 256, CB = TN * CPR / 256;  // chunks per thread (VEC)
-    constexpr int LA = TM * KT / 256, LB = TN * KT / 256;    // elements per thread (!VEC)
-    static_assert(!VEC || (CA >= 1 && CB >= 1), "every thread loads a chunk");
+    // chunks (VEC) or elements per thread; an A slice smaller than 256
+    // chunks leaves the threads past its end idle (tiles of 8 rows)
+    constexpr int CA = (TM * CPR + 255) / 256, CB = TN * CPR / 256;
+    constexpr int LA = (TM * KT + 255) / 256, LB = TN * KT / 256;
+    static_assert(VEC ? TN * CPR % 256 == 0 : TN * KT % 256 == 0, "B slices in whole passes");
+    static_assert(VEC ? (TM * CPR % 256 == 0 || TM * CPR < 256) : (TM * KT % 256 == 0 || TM * KT < 256),
+                  "A slice: whole passes or one partial pass");
     __shared__ __attribute__((aligned(16))) uint16_t As[TM][P];
     __shared__ __attribute__((aligned(16))) uint16_t Bs[TN][P];
 
@@ -57,8 +62,9 @@ __global__ __launch_bounds__(256) void naive_gemm_kernel(const uint16_t* __restr
 #pragma unroll
             for (int e = 0; e < CA; ++e) {
                 const uint32_t idx = e * 256u + t, r = idx / CPR, k = k0 + (idx % CPR) * 8, m = m0 + r;
-                va[e] = (m < M && k < K) ? *reinterpret_cast<const u32x4_t*>(A + (size_t)m * lda + k)
-                                         : u32x4_t{0u, 0u, 0u, 0u};
+                va[e] = (idx < (uint32_t)(TM * CPR) && m < M && k < K)
+                            ? *reinterpret_cast<const u32x4_t*>(A + (size_t)m * lda + k)
+                            : u32x4_t{0u, 0u, 0u, 0u};
             }
 #pragma unroll
             for (int e = 0; e < CB; ++e) {
@@ -70,7 +76,7 @@ __global__ __launch_bounds__(256) void naive_gemm_kernel(const uint16_t* __restr
 #pragma unroll
             for (int e = 0; e < LA; ++e) {
                 const uint32_t idx = e * 256u + t, r = idx / KT, k = k0 + idx % KT, m = m0 + r;
-                sa[e] = (m < M && k < K) ? A[(size_t)m * lda + k] : (uint16_t)0;
+                sa[e] = (idx < (uint32_t)(TM * KT) && m < M && k < K) ? A[(size_t)m * lda + k] : (uint16_t)0;
             }
 #pragma unroll
             for (int e = 0; e < LB; ++e) {
@@ -84,7 +90,8 @@ __global__ __launch_bounds__(256) void naive_gemm_kernel(const uint16_t* __restr
 #pragma unroll
             for (int e = 0; e < CA; ++e) {
                 const uint32_t idx = e * 256u + t;
-                *reinterpret_cast<u32x4_t*>(&As[idx / CPR][(idx % CPR) * 8]) = va[e];
+                if (idx < (uint32_t)(TM * CPR))
+                    *reinterpret_cast<u32x4_t*>(&As[idx / CPR][(idx % CPR) * 8]) = va[e];
             }
 #pragma unroll
             for (int e = 0; e < CB; ++e) {
@@ -95,7 +102,7 @@ __global__ __launch_bounds__(256) void naive_gemm_kernel(const uint16_t* __restr
 #pragma unroll
             for (int e = 0; e < LA; ++e) {
                 const uint32_t idx = e * 256u + t;
-                As[idx / KT][idx % KT] = sa[e];
+                if (idx < (uint32_t)(TM * KT)) As[idx / KT][idx % KT] = sa[e];
             }
 #pragma unroll
             for (int e = 0; e < LB; ++e) {
@@ -182,8 +189,12 @@ hipError_t launch_gemm_naive(const void* A, const void* B, float* C, uint32_t M,
     // Deep K slices cut the number of load round trips a chain waits for.
     if (N <= 32)
         launch_cfg<16, 16, 1, 1, 512>(vec, A, B, C, M, N, K, lda, ldb, ldc, st);
+    else if (M <= 8)
+        launch_cfg<8, 256, 2, 4, 64>(vec, A, B, C, M, N, K, lda, ldb, ldc, st);
     else if (M <= 16)
         launch_cfg<16, 128, 2, 4, 128>(vec, A, B, C, M, N, K, lda, ldb, ldc, st);
+    else if (M <= 32)
+        launch_cfg<32, 128, 4, 4, 64>(vec, A, B, C, M, N, K, lda, ldb, ldc, st);
     else
         launch_cfg<64, 64, 4, 4, 64>(vec, A, B, C, M, N, K, lda, ldb, ldc, st);
     return hipGetLastError();
