@@ -205,8 +205,11 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
         wrow[nt] = W + (size_t)n * rb;
     }
     const uint16_t* xrow[MT];
-    // rows [m0, m0 + 16 MT) of x and y (M split over gridDim.z)
-    const uint32_t m0 = blockIdx.z * 16u * MT;
+    // rows [m0, m0 + mstep) of y (M split over gridDim.z); x rows past that
+    // range are loaded (clamped into x) but their outputs are not stored
+    const uint32_t mstep = (M + gridDim.z - 1) / gridDim.z;
+    const uint32_t m0 = blockIdx.z * mstep;
+    const uint32_t m1 = min(M, m0 + mstep);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) xrow[mt] = X + (size_t)min(m0 + mt * 16u + j, M - 1u) * K;
 
@@ -450,7 +453,7 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
         const uint32_t nt = tm / MT, mt = tm % MT;
         const uint32_t n = n0 + nt * 16u + (ln & 15u);
         const uint32_t m = m0 + mt * 16u + 4u * (ln >> 4) + e4;
-        if (n < N && m < M) {
+        if (n < N && m < m1) {
             if (gridDim.y == 1)
                 store_out(Y, (size_t)m * N + n, v, bf);
             else
@@ -576,17 +579,17 @@ hipError_t by_shape(uint32_t G, const void* X, const void* W, const void* S, con
             return by_group<MODE, 2, 4, 4>(G, X, W, S, B, Y, M, N, K, out_bf16, sk, st);
         }
     }
-    // M split above M = 16 when the doubled grid still fits one round of
-    // 256 workgroups: one 16-row m-tile per workgroup (gridDim.z), the
-    // weights read once per m-tile (from L2 for the second). Every output
-    // element is computed as without the split. Measured at M = 32, K =
-    // 2048: N = 2048 7.09 -> 5.23 us (fused 7.36 -> 5.73, bf16 9.85 -> 8.04),
-    // N = 512 6.79 -> 5.12; at N = 3072 (192 -> 384 workgroups) it was
-    // slower, bf16 10.3 -> 14.2 us.
+    // M split above M = 8 when the doubled grid still fits one round of
+    // 256 workgroups: the rows go to two workgroups (gridDim.z) of one
+    // 16-row m-tile each, half of it idle up to M = 16, and the second reads
+    // the weights from L2. Every output element is computed as without the
+    // split. Measured at M = 32, K = 2048: N = 2048 7.09 -> 5.23 us (fused
+    // 7.36 -> 5.73, bf16 9.85 -> 8.04), N = 512 6.79 -> 5.12; at N = 3072
+    // (192 -> 384 workgroups) it was slower, bf16 10.3 -> 14.2 us.
     uint32_t mz = 1;
     const uint32_t wgs = (N + 16u * nt - 1) / (16u * nt) * sk;
-    if (M > 16 && wgs <= 128) mz = 2;
-    if (const char* e = getenv("MIORI_SKINNY_MZ")) mz = (atoi(e) == 2 && M > 16) ? 2 : 1;
+    if (M > 8 && wgs <= 128) mz = 2;
+    if (const char* e = getenv("MIORI_SKINNY_MZ")) mz = (atoi(e) == 2 && M > 8) ? 2 : 1;
     if (M <= 16 || mz == 2)
         return by_nt<MODE, 1>(nt, G, X, W, S, B, Y, M, N, K, out_bf16, sk, st, mz);
     return by_nt<MODE, 2>(nt, G, X, W, S, B, Y, M, N, K, out_bf16, sk, st);
