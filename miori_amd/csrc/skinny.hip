@@ -38,6 +38,7 @@
 
 #include <stdlib.h>
 
+#include <algorithm>
 #include <type_traits>
 
 namespace miori {
@@ -58,12 +59,18 @@ struct Sk {
     static constexpr int WL = MODE == BF16 ? STEPS : 1;        // 16-byte weight loads per n-tile
     // k-steps folded together (one quantisation group inside the block)
     static constexpr int SPF = !EXACT ? STEPS : ((G < KB ? G : KB) / 32);
+    // x staged in LDS once per workgroup (8-bit, the four-wave two-n-tile
+    // form used up to M = 8, whole K <= 2048): x fragments are then LDS
+    // reads, which leaves the vector memory path to the weight stream. XR:
+    // LDS row stride in bf16 (16-byte pad between rows).
+    static constexpr bool XL = MODE == Q8X && NWV == 4 && MT == 1 && NT == 2 && NBW * NWV * KB <= 2048;
+    static constexpr int XR = NBW * NWV * KB + 8;
     // registers (dwords) per block slot, to size the pipeline depth
-    static constexpr int REGS = NT * WL * 4 + MT * STEPS * 4;
+    static constexpr int REGS = NT * WL * 4 + (XL ? 0 : MT * STEPS * 4);
     static constexpr int PD0 = 136 / REGS;
     static constexpr int PD = PD0 < 2 ? 2 : (PD0 > 4 ? 4 : PD0);   // blocks in flight per wave
     static constexpr int TOT = NT * MT * 4 * 64;                  // partial floats per wave
-    static constexpr int L = NT * WL + MT * STEPS;                // loads per block
+    static constexpr int L = NT * WL + (XL ? 0 : MT * STEPS);     // loads per block
     // scale / bias tiles of the workgroup's rows in LDS (all K/G groups of up
     // to NBW * NWV blocks), rounded up to whole 1 KiB DMA chunks
     static constexpr int NB = 16 * NT;
@@ -213,9 +220,26 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) xrow[mt] = X + (size_t)min(m0 + mt * 16u + j, M - 1u) * K;
 
+    // x tile in LDS (C::XL): rows m0 .. m1-1 (one K split, whole K), one 1 KiB
+    // DMA per (row, 512-k chunk), issued before the first block so that
+    // block's wait covers it. Lanes of rows past m1 read row m1-1: their
+    // outputs are not stored.
+    extern __shared__ __attribute__((aligned(16))) uint8_t xdyn[];
+    typedef __attribute__((address_space(3))) const u32x4_t* lds_v4;
+    const uint32_t xrows = min(16u, m1 - m0);
+    const lds_v4 xl_row = (lds_v4)(xdyn + min(j, xrows - 1u) * (uint32_t)C::XR * 2u);
+    if constexpr (C::XL) {
+        const uint32_t nch = K / 512u;
+        for (uint32_t u = wave; u < xrows * nch; u += NWV) {
+            const uint32_t r = u / nch, ch = u % nch;
+            dma16(X + (size_t)(m0 + r) * K + ch * 512u + lane * 8u,
+                  xdyn + r * (uint32_t)C::XR * 2u + ch * 1024u);
+        }
+    }
+
     // block slots
     u32x4_t wr[C::DEPTH][NT][C::WL];
-    u32x4_t xr[C::DEPTH][MT][C::STEPS];
+    u32x4_t xr[C::XL ? 1 : C::DEPTH][MT][C::STEPS];
 
     auto issue = [&](uint32_t blk, auto slot_c) {
         constexpr int sl = decltype(slot_c)::value;
@@ -231,11 +255,13 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
                 ld16nt(wr[sl][nt][0], wrow[nt] + byte);
             }
         }
+        if constexpr (!C::XL) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+            for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int r = 0; r < C::STEPS; ++r)
-                ld16(xr[sl][mt][r], xrow[mt] + k0 + kmap<MODE, G>(c, r));
+                for (int r = 0; r < C::STEPS; ++r)
+                    ld16(xr[sl][mt][r], xrow[mt] + k0 + kmap<MODE, G>(c, r));
+        }
     };
 
     f32x4_t acc[NT][MT];
@@ -268,11 +294,17 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
         constexpr int i = decltype(i_c)::value;
         constexpr int sl = i % C::DEPTH;
         bf16x8_t xf[MT][C::STEPS];
+        // (the block's k base inside the workgroup's range, for the LDS x tile)
+        const uint32_t kx = min(b0 + (uint32_t)i, nblk - 1u) * C::KB;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int r = 0; r < C::STEPS; ++r) {
-                u32x4_t d = xr[sl][mt][r];
+                u32x4_t d;
+                if constexpr (C::XL)
+                    d = xl_row[(kx + kmap<MODE, G>(c, r)) / 8u];
+                else
+                    d = xr[sl][mt][r];
                 if constexpr (!C::EXACT) {
                     d[0] = valid ? d[0] : 0u;
                     d[1] = valid ? d[1] : 0u;
@@ -402,11 +434,14 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
 #pragma unroll
             for (int q = 0; q < C::WL; ++q) tie(wr[sl][nt][q]);
         }
+        if constexpr (!C::XL) {
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+            for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int r = 0; r < C::STEPS; ++r) tie(xr[sl][mt][r]);
-        if constexpr (i == 0 && MODE != BF16) barrier_lds();  // scale/bias tiles landed (all waves)
+                for (int r = 0; r < C::STEPS; ++r) tie(xr[sl][mt][r]);
+        }
+        // scale/bias tiles (and the x tile) landed for all waves
+        if constexpr (i == 0 && MODE != BF16) barrier_lds();
         // keep each block's work (and its scale reads) inside its step
         __builtin_amdgcn_sched_barrier(0);
         compute(ic<i>{}, (uint32_t)i < nb);
@@ -474,8 +509,15 @@ hipError_t launch_sk(const void* X, const void* W, const void* S, const void* B,
         const hipError_t e = workspace_get(st, (size_t)SK * M * N * 4, &part);
         if (e != hipSuccess) return e;
     }
+    using C = Sk<MODE, MT, NT, G, NBW, NWV>;
+    size_t xbytes = 0;
+    if constexpr (C::XL) {
+        // whole 1 KiB x chunks per row, 16-byte aligned rows, no K split
+        if (SK != 1 || K % 512 != 0 || ((uintptr_t)X & 15) != 0) return hipErrorInvalidValue;
+        xbytes = (size_t)std::min(16u, (M + MZ - 1) / MZ) * C::XR * 2;
+    }
     hipLaunchKernelGGL((skinny_kernel<MODE, MT, NT, G, NBW, NWV>), dim3(nwg, SK, MZ), dim3(NWV * 64),
-                       0, st, (const uint16_t*)X, (const uint8_t*)W, (const uint16_t*)S,
+                       xbytes, st, (const uint16_t*)X, (const uint8_t*)W, (const uint16_t*)S,
                        (const uint16_t*)B, Y, M, N, K, out_bf16, part);
     if (SK > 1) {
         const hipError_t e = hipGetLastError();
@@ -567,11 +609,14 @@ hipError_t by_shape(uint32_t G, const void* X, const void* W, const void* S, con
     // 8-bit M=32 140 -> 117 us, M=16 90 -> 85, M=8 80.5 -> 78.7; 4-bit at
     // N = 65536 M=32 45.5 -> 38.5 us, M=8 25.0 -> 24.5 (four n-tiles: 26.4).
     // Needs the whole K in 8 blocks per wave and no K split.
+    // Up to M = 8 at K <= 2048 the 8-bit four-wave form stages x in LDS,
+    // which needs whole 512-element chunks of 16-byte aligned rows.
+    const bool nw4_ok = sk == 1 && K / kb <= 32 &&
+                        (MODE != Q8X || M > 8 || K > 2048 || (K % 512 == 0 && ((uintptr_t)X & 15) == 0));
     int nw = 8;
-    if ((MODE == Q4X || MODE == Q8X) && sk == 1 && N >= 32768 && K / kb <= 32 &&
-        !getenv("MIORI_SKINNY_NT"))
+    if ((MODE == Q4X || MODE == Q8X) && N >= 32768 && nw4_ok && !getenv("MIORI_SKINNY_NT"))
         nw = 4;
-    if (const char* e = getenv("MIORI_SKINNY_NW")) nw = (atoi(e) == 4 && sk == 1 && K / kb <= 32) ? 4 : 8;
+    if (const char* e = getenv("MIORI_SKINNY_NW")) nw = (atoi(e) == 4 && nw4_ok) ? 4 : 8;
     if constexpr (MODE == Q4X || MODE == Q8X) {
         if (nw == 4) {
             if (M <= 8) return by_group<MODE, 1, 2, 4>(G, X, W, S, B, Y, M, N, K, out_bf16, sk, st);

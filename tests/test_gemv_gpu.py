@@ -194,3 +194,20 @@ def test_batched_skinny_four_wave(dev, bits, M, N, K, G):
     y = _run(lin, xd, M, torch.bfloat16)
     ref = oracle.gemv_f64(w.q, w.s, w.b, x, bits, K, G, nthreads=NT)
     check_close(y, ref, f"gemv{bits}_b four-wave M={M} G={G}")
+
+
+def test_gemv8_batched_lds_x_fallback(dev):
+    """Up to M = 8 the 8-bit vocabulary-sized form stages x in LDS in whole
+    512-element chunks; K = 1280 takes the eight-wave form instead, with the
+    oracle's result. (A misaligned x is rejected by the entry point.)"""
+    M, N, K, G = 7, 32768, 1280, 32
+    say(f"gemv8_b LDS-x fallback N={N} K={K} G={G}")
+    w, lin = weights(N, K, G, 8, seed=K + G, dev=dev)
+    x, xd = acts(M, K, seed=31, dev=dev)
+    y = _run(lin, xd, M, torch.bfloat16)
+    ref = oracle.gemv_f64(w.q, w.s, w.b, x, 8, K, G, nthreads=NT)
+    check_close(y, ref, f"gemv8_b M={M} N={N} K={K}")
+    buf = torch.empty(M * K + 8, dtype=xd.dtype, device=dev)
+    xm = buf[1:1 + M * K].view(M, K)
+    with pytest.raises(MioriError):
+        _run(lin, xm, M, torch.bfloat16)
