@@ -1,6 +1,7 @@
 // Shared device helpers for the gfx950 kernels of libmiori_hip.so.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <stdlib.h>
 #include <stdint.h>
 
 namespace miori {
@@ -164,6 +165,14 @@ __device__ __forceinline__ int reduce_value(int RV, int i, int row) {
     if (RV == 2) return row >> 1;
     const int H = RV / 2;
     return 2 * i + (row & 1) + ((row >> 1) ? H : 0);
+}
+
+// Tuning override MIORI_*: its integer value, or dflt when unset. Call sites
+// keep the result in a function-local static, so each variable is read once
+// per process (later changes to the environment are not seen).
+inline int tuning_env(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return (v && *v) ? atoi(v) : dflt;
 }
 
 // ---- direct-to-LDS DMA and barriers (gfx950)

@@ -545,7 +545,7 @@ hipError_t launch_cfg(const void* A, const void* B, const void* q, const void* s
     const uint32_t tiles_m = (M + BM - 1) / BM;
     const uint32_t tiles_n = (N + BN - 1) / BN;
     const uint32_t ntiles = tiles_m * tiles_n;
-    const int remap = getenv("MIORI_GEMM_REMAP") ? atoi(getenv("MIORI_GEMM_REMAP")) : 1;
+    static const int remap = tuning_env("MIORI_GEMM_REMAP", 1);
     float* part = nullptr;
     if (SK > 1) {
         const hipError_t e = workspace_get(st, (size_t)SK * M * N * 4, &part);
@@ -636,7 +636,8 @@ hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* 
     int tile = pick_tile_256x128(M, N, K);
     if (!q && huge >= 192) tile = 2;
     else if (K <= 4096 && t64 <= 512) tile = q ? 3 : 4;
-    if (const char* e = getenv("MIORI_GEMM_TILE")) tile = atoi(e);
+    static const int e_tile = tuning_env("MIORI_GEMM_TILE", -1);
+    if (e_tile >= 0) tile = e_tile;
     if (tile == 2 && !q) return launch_cfg<256, 256, false, 64>(A, B, q, s, b, C, M, N, K, out_bf16, 1, st);
     if (tile == 2) tile = pick_tile_256x128(M, N, K);  // fused: no 256x256 variant
     // (64x64 splits as the 64x128 grid, the fused path's tile)
@@ -647,7 +648,8 @@ hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* 
     // count splits alike (rows of a small product equal those of a larger one)
     const uint64_t tile_elems = (uint64_t)tbm * tbn;
     uint32_t SK = pick_split(ntiles, K / 64, ntiles * tile_elems);
-    if (const char* e = getenv("MIORI_GEMM_SPLIT")) SK = (uint32_t)atoi(e);
+    static const int e_split = tuning_env("MIORI_GEMM_SPLIT", -1);
+    if (e_split >= 0) SK = (uint32_t)e_split;
     if (SK < 1) SK = 1;
     if (SK > 16) SK = 16;
     if (SK > K / 64) SK = K / 64;

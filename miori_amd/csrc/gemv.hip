@@ -401,10 +401,6 @@ hipError_t dispatch_mr(int mr, int rows, int cpl, const void* q, const void* s, 
     return hipErrorInvalidValue;
 }
 
-int env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return (v && *v) ? atoi(v) : dflt;
-}
 
 }  // namespace
 
@@ -426,7 +422,7 @@ hipError_t launch_gemv_valu(int bits, const void* q, const void* s, const void* 
     int cpl;
     gemv_split(bits, K, &S, &cpl);
     // rows per wave for M = 1 (MIORI_GEMV_ROWS overrides it for tuning sweeps)
-    const int rows_m1 = env_int("MIORI_GEMV_ROWS", 4);
+    static const int rows_m1 = tuning_env("MIORI_GEMV_ROWS", 4);
     const int mr_max = cpl == 1 ? 4 : (cpl == 2 ? 2 : 1);
     const size_t ybytes = out_bf16 ? 2 : 4;
     for (uint32_t m0 = 0; m0 < M; m0 += mr_max) {
@@ -457,10 +453,7 @@ hipError_t launch_gemv_fused(int xm, const void* q, const void* s, const void* b
     // give 512 or more workgroups (N=8192 at K=2048, N=2048 at K=7680);
     // smaller grids keep 4 rows so the weight stream has enough waves.
     // MIORI_FUSED_ROWS=4|8 overrides the choice for tuning sweeps.
-    static const int r_env = [] {
-        const char* v = getenv("MIORI_FUSED_ROWS");
-        return v ? atoi(v) : 0;
-    }();
+    static const int r_env = tuning_env("MIORI_FUSED_ROWS", 0);
     const int R = r_env == 8 || r_env == 4 ? r_env
                   : (N + 4u * (4u / S) - 1) / (4u * (4u / S)) >= 512u ? 8 : 4;
     const uint32_t rows_per_wg = R * (4u / S);

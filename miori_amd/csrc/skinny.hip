@@ -593,10 +593,15 @@ hipError_t by_shape(uint32_t G, const void* X, const void* W, const void* S, con
         sk = 4;
         nt = 2;
     }
-    if (const char* e = getenv("MIORI_SKINNY_NT")) nt = atoi(e);
+    // tuning overrides (MIORI_SKINNY_*), read once per process
+    static const int e_nt = tuning_env("MIORI_SKINNY_NT", -1);
+    static const int e_split = tuning_env("MIORI_SKINNY_SPLIT", -1);
+    static const int e_nw = tuning_env("MIORI_SKINNY_NW", -1);
+    static const int e_mz = tuning_env("MIORI_SKINNY_MZ", -1);
+    if (e_nt >= 0) nt = e_nt;
     // N a multiple of 16 so the partials' reduction covers whole 8-element
     // groups; the split must divide the K blocks
-    if (const char* e = getenv("MIORI_SKINNY_SPLIT")) sk = (uint32_t)atoi(e);
+    if (e_split >= 0) sk = (uint32_t)e_split;
     const uint32_t kb = MODE == Q8X ? 64u : 128u;
     if (sk < 1 || N % 16 != 0) sk = 1;
     // (a function of N and K only, so the fused 4-bit and the bf16 products
@@ -614,9 +619,9 @@ hipError_t by_shape(uint32_t G, const void* X, const void* W, const void* S, con
     const bool nw4_ok = sk == 1 && K / kb <= 32 &&
                         (MODE != Q8X || M > 8 || K > 2048 || (K % 512 == 0 && ((uintptr_t)X & 15) == 0));
     int nw = 8;
-    if ((MODE == Q4X || MODE == Q8X) && N >= 32768 && nw4_ok && !getenv("MIORI_SKINNY_NT"))
+    if ((MODE == Q4X || MODE == Q8X) && N >= 32768 && nw4_ok && e_nt < 0)
         nw = 4;
-    if (const char* e = getenv("MIORI_SKINNY_NW")) nw = (atoi(e) == 4 && nw4_ok) ? 4 : 8;
+    if (e_nw >= 0) nw = (e_nw == 4 && nw4_ok) ? 4 : 8;
     if constexpr (MODE == Q4X || MODE == Q8X) {
         if (nw == 4) {
             if (M <= 8) return by_group<MODE, 1, 2, 4>(G, X, W, S, B, Y, M, N, K, out_bf16, sk, st);
@@ -634,7 +639,7 @@ hipError_t by_shape(uint32_t G, const void* X, const void* W, const void* S, con
     uint32_t mz = 1;
     const uint32_t wgs = (N + 16u * nt - 1) / (16u * nt) * sk;
     if (M > 8 && wgs <= 128) mz = 2;
-    if (const char* e = getenv("MIORI_SKINNY_MZ")) mz = (atoi(e) == 2 && M > 8) ? 2 : 1;
+    if (e_mz >= 0) mz = (e_mz == 2 && M > 8) ? 2 : 1;
     if (M <= 16 || mz == 2)
         return by_nt<MODE, 1>(nt, G, X, W, S, B, Y, M, N, K, out_bf16, sk, st, mz);
     return by_nt<MODE, 2>(nt, G, X, W, S, B, Y, M, N, K, out_bf16, sk, st);
