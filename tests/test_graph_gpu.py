@@ -33,6 +33,16 @@ def _case(name, dev):
         _, x = acts(M, 2048, seed=16 + M, dev=dev)
         y = torch.empty((M, 2048), dtype=torch.bfloat16, device=dev)
         return (lambda: ops.gemv4_b(lin.q, lin.s, lin.b, x, y, 2048, 2048, M)), y
+    if name.startswith("gemv8_b_vocab") or name.startswith("gemv4_b_vocab"):
+        # vocabulary-sized N: the four-wave skinny forms (8-bit M <= 8 stages x in LDS)
+        bits = 8 if name.startswith("gemv8") else 4
+        M = int(name.split("_m")[1])
+        N, K = 32768, 2048
+        _, lin = weights(N, K, 64, bits, seed=40 + M, dev=dev)
+        _, x = acts(M, K, seed=41 + M, dev=dev)
+        y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        f = ops.gemv8_b if bits == 8 else ops.gemv4_b
+        return (lambda: f(lin.q, lin.s, lin.b, x, y, N, K, M)), y
     if name.startswith("gemm_bf16"):
         M, N, K = {"gemm_bf16_splitk": (256, 2560, 2048), "gemm_bf16_256": (1472, 8192, 2048),
                    "gemm_bf16_skinny": (24, 2048, 2048)}[name]
@@ -71,7 +81,8 @@ def _case(name, dev):
     raise KeyError(name)
 
 
-CASES = ["gemv4", "gemv8", "gemv4_b_m4", "gemv4_b_m8", "gemv4_b_m32", "gemm_bf16_splitk",
+CASES = ["gemv4", "gemv8", "gemv4_b_m4", "gemv4_b_m8", "gemv4_b_m32", "gemv8_b_vocab_m8",
+         "gemv4_b_vocab_m24", "gemm_bf16_splitk",
          "gemm_bf16_256", "gemm_bf16_skinny", "gemm_q4", "gemm_naive", "rmsnorm_gemv4",
          "silu_mul_gemv4", "dequant_tile"]
 
