@@ -54,6 +54,8 @@ def _parse():
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--all", action="store_true", help="also time every benchmark config")
+    p.add_argument("--config", type=int, default=None, choices=range(5),
+                   help="also time the cases of one benchmark config (0-4)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--calib-copy", action="store_true",
@@ -427,45 +429,57 @@ def main():
     }
     if args.calib_copy:
         calib_copy(torch, dev)
-    if args.all:
-        out["configs"] = run_all(torch, ops, synth, oracle, dev, timer)
+    if args.all or args.config is not None:
+        out["configs"] = run_all(torch, ops, synth, oracle, dev, timer,
+                                 only=None if args.all else args.config)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(out), flush=True)
 
 
-def run_all(torch, ops, synth, oracle, dev, timer):
+def run_all(torch, ops, synth, oracle, dev, timer, only=None):
+    """Every benchmark config, or only config `only` (0-4; the next-row cases,
+    fused decode and gemm_naive, run with the full set)."""
     rows = []
     st, wu = 100, 10
-    rows.append(dict(config=0, **gemv_case(torch, ops, synth, dev, 4, 1, 8192, 2048, 64,
-                                           torch.bfloat16, timer, st, wu)))
-    for (K, N) in [(2048, 2048), (2048, 512), (2048, 8192), (8192, 2048)]:
-        for M in (2, 4, 8, 16, 32):
-            rows.append(dict(config=1, **gemv_case(torch, ops, synth, dev, 4, M, N, K, 64,
-                                                   torch.bfloat16, timer, st, wu)))
-            print(f"[bench] {rows[-1]}", file=sys.stderr, flush=True)
-    for M in (1, 8, 32):
-        rows.append(dict(config=2, **gemv_case(torch, ops, synth, dev, 8, M, 131072, 2048, 64,
-                                               torch.bfloat16, timer, 20, 3)))
-        print(f"[bench] {rows[-1]}", file=sys.stderr, flush=True)
-    for M in (1024, 32):
-        for stacked in (False, True):
-            rows.append(chain_case(torch, ops, synth, dev, M, timer, stacked=stacked))
-            print(f"[bench] {rows[-1]}", file=sys.stderr, flush=True)
+
+    def want(c):
+        return only is None or only == c
+
+    def emit(row):
+        rows.append(row)
+        print(f"[bench] {row}", file=sys.stderr, flush=True)
+
+    if want(0):
+        emit(dict(config=0, **gemv_case(torch, ops, synth, dev, 4, 1, 8192, 2048, 64,
+                                        torch.bfloat16, timer, st, wu)))
+    if want(1):
+        for (K, N) in [(2048, 2048), (2048, 512), (2048, 8192), (8192, 2048)]:
+            for M in (2, 4, 8, 16, 32):
+                emit(dict(config=1, **gemv_case(torch, ops, synth, dev, 4, M, N, K, 64,
+                                                torch.bfloat16, timer, st, wu)))
+    if want(2):
+        for M in (1, 8, 32):
+            emit(dict(config=2, **gemv_case(torch, ops, synth, dev, 8, M, 131072, 2048, 64,
+                                            torch.bfloat16, timer, 20, 3)))
+    if want(4):
+        for M in (1024, 32):
+            for stacked in (False, True):
+                emit(chain_case(torch, ops, synth, dev, M, timer, stacked=stacked))
     for fused in (False, True):
+        if not want(4 if fused else 3):
+            continue
         for M in (256, 1024, 1472):
             for (K, N) in [(2048, 8192), (8192, 2048), (2048, 2560)]:
-                rows.append(dict(config=4 if fused else 3,
-                                 **gemm_case(torch, ops, synth, oracle, dev, M, N, K, fused,
-                                             timer, 30, 3)))
-                print(f"[bench] {rows[-1]}", file=sys.stderr, flush=True)
-    for (K, N) in [(2048, 2048), (2048, 8192), (7680, 2048), (8192, 2048)]:
-        rows.append(dict(row="fused-decode", **fused_decode_case(torch, ops, synth, dev, N, K,
-                                                                timer, st, wu)))
-        print(f"[bench] {rows[-1]}", file=sys.stderr, flush=True)
-    for (M, N, K) in [(1, 16, 2048), (32, 16, 2048), (8, 131072, 2048), (32, 131072, 2048)]:
-        rows.append(dict(row="gemm_naive", **naive_case(torch, ops, dev, M, N, K, timer, 20, 3)))
-        print(f"[bench] {rows[-1]}", file=sys.stderr, flush=True)
+                emit(dict(config=4 if fused else 3,
+                          **gemm_case(torch, ops, synth, oracle, dev, M, N, K, fused,
+                                      timer, 30, 3)))
+    if only is None:
+        for (K, N) in [(2048, 2048), (2048, 8192), (7680, 2048), (8192, 2048)]:
+            emit(dict(row="fused-decode", **fused_decode_case(torch, ops, synth, dev, N, K,
+                                                             timer, st, wu)))
+        for (M, N, K) in [(1, 16, 2048), (32, 16, 2048), (8, 131072, 2048), (32, 131072, 2048)]:
+            emit(dict(row="gemm_naive", **naive_case(torch, ops, dev, M, N, K, timer, 20, 3)))
     return rows
 
 
