@@ -394,7 +394,13 @@ hipError_t dispatch_mr(int mr, int rows, int cpl, const void* q, const void* s, 
         }
     }
     switch (mr) {
-        case 2: return dispatch_cpl<BITS, 2, 2>(cpl, q, s, b, x, y, N, K, G, S, out_bf16, st);
+        // two rows of x: four weight rows per wave from N = 4096 (half the x
+        // loads per weight byte; measured M=2 N=8192 4.74 -> 4.28 us, K=8192
+        // 5.98 -> 4.86, 8-bit lm_head 65-70 -> 48-54), two below (a grid of
+        // half the workgroups was 6-9% slower at N <= 2048)
+        case 2:
+            return N >= 4096 ? dispatch_cpl<BITS, 2, 4>(cpl, q, s, b, x, y, N, K, G, S, out_bf16, st)
+                             : dispatch_cpl<BITS, 2, 2>(cpl, q, s, b, x, y, N, K, G, S, out_bf16, st);
         case 3: return dispatch_cpl<BITS, 3, 2>(cpl, q, s, b, x, y, N, K, G, S, out_bf16, st);
         case 4: return dispatch_cpl<BITS, 4, 2>(cpl, q, s, b, x, y, N, K, G, S, out_bf16, st);
     }
