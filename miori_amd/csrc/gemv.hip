@@ -106,8 +106,8 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(
     constexpr uint32_t E = (BITS == 4) ? 32u : 16u;  // elements per 16-byte chunk
     constexpr int XL = (BITS == 4) ? 4 : 2;          // 16-byte x loads per chunk
     constexpr int RV0 = R * MR;
-    constexpr int RV = RV0 <= 1 ? 1 : RV0 <= 2 ? 2 : RV0 <= 4 ? 4 : 8;
-    static_assert(RV0 <= 8, "at most 8 row sums per wave");
+    constexpr int RV = RV0 <= 1 ? 1 : RV0 <= 2 ? 2 : RV0 <= 4 ? 4 : RV0 <= 8 ? 8 : 16;
+    static_assert(RV0 <= 16, "at most 16 row sums per wave");
     __shared__ float red[4][RV];
 
     const uint32_t lane = threadIdx.x & 63u;
@@ -401,8 +401,12 @@ hipError_t dispatch_mr(int mr, int rows, int cpl, const void* q, const void* s, 
         case 2:
             return N >= 4096 ? dispatch_cpl<BITS, 2, 4>(cpl, q, s, b, x, y, N, K, G, S, out_bf16, st)
                              : dispatch_cpl<BITS, 2, 2>(cpl, q, s, b, x, y, N, K, G, S, out_bf16, st);
-        case 3: return dispatch_cpl<BITS, 3, 2>(cpl, q, s, b, x, y, N, K, G, S, out_bf16, st);
-        case 4: return dispatch_cpl<BITS, 4, 2>(cpl, q, s, b, x, y, N, K, G, S, out_bf16, st);
+        case 3:
+            return N >= 4096 ? dispatch_cpl<BITS, 3, 4>(cpl, q, s, b, x, y, N, K, G, S, out_bf16, st)
+                             : dispatch_cpl<BITS, 3, 2>(cpl, q, s, b, x, y, N, K, G, S, out_bf16, st);
+        case 4:
+            return N >= 4096 ? dispatch_cpl<BITS, 4, 4>(cpl, q, s, b, x, y, N, K, G, S, out_bf16, st)
+                             : dispatch_cpl<BITS, 4, 2>(cpl, q, s, b, x, y, N, K, G, S, out_bf16, st);
     }
     return hipErrorInvalidValue;
 }

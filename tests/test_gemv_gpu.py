@@ -111,12 +111,12 @@ def test_gemv4_batched_large_shapes(dev, M, N, K):
     check_close(y[:, rows], ref, f"gemv4_b M={M} {N}x{K}")
 
 
-@pytest.mark.parametrize("bits,N,M", [(4, 2048, 4), (4, 8192, 2), (4, 4096, 3), (8, 16384, 2)])
+@pytest.mark.parametrize("bits,N,M", [(4, 2048, 4), (4, 8192, 2), (4, 4096, 3), (4, 8192, 4), (8, 16384, 2), (8, 8192, 4)])
 def test_gemv4_batched_rows_equal_single(dev, bits, N, M):
     """Each batched row is the single-row product: bit-identical for M <= 4,
     the reference's guarantee (shaders/batch.metal:142-144), whatever the
-    rows per wave (two rows of x take four weight rows per wave from
-    N = 4096)."""
+    rows per wave (two to four rows of x take four weight rows per wave
+    from N = 4096)."""
     K, G = 2048, 64
     say(f"gemv{bits}_b rows == gemv{bits} N={N} M={M}")
     w, lin = weights(N, K, G, bits, seed=5, dev=dev)
