@@ -9,15 +9,18 @@
 // +0, the reference kernel's accumulation, so results are reproducible bit
 // for bit by a sequential fmaf loop on the CPU.
 //
-// Structure: 256 threads own a TM x TN output tile as RM x RN register tiles.
+// Structure: 256 threads own a TM x TN output tile, RM x RN outputs each
+// (rows TM/RM apart, columns TN/RN apart).
 // K advances in KT-deep slices; each slice of A and B is loaded coalesced
 // (16-byte chunks along k when strides allow) into row-major LDS rows padded
 // by 16 bytes, and the next slice's loads are in flight while the current one
-// is computed. A thread reads 8 consecutive k of each of its rows as one
-// 16-byte LDS read and runs the 8 FMAs of every chain in k order. The chains
+// is computed. A is converted to fp32 as it is stored (each A element feeds
+// TN/RN threads); B stays bf16 and is converted at use. A thread reads 8
+// consecutive k of each of its B rows as one 16-byte LDS read (two for an A
+// row) and runs the 8 FMAs of every chain in k order. The chains
 // cannot be split over k, so the slice depth sets how many load round trips
 // a chain waits for. Tile shapes: 64 x 64 (KT 64) for general M; 8 x 256
-// (KT 64), 16 x 128 (KT 128) and 32 x 128 (KT 64) for M <= 8 / 16 / 32 (the
+// (KT 64), 16 x 128 (KT 128) and 32 x 256 (KT 64) for M <= 8 / 16 / 32 (the
 // batch lm_head, where a taller tile would spend half or more of its FMAs on
 // padding rows); 16 x 16 (KT 512) for N <= 32 (gate_proj N=16). Element
 // loads (any stride) use a quarter of the slice depth.
@@ -38,7 +41,8 @@ __global__ __launch_bounds__(256) void naive_gemm_kernel(const uint16_t* __restr
                                                          uint32_t ldb, uint32_t ldc) {
     static_assert((TM / RM) * (TN / RN) == 256, "one register tile per thread");
     static_assert(KT % 8 == 0, "8-k chunks");
-    constexpr int P = KT + 8;                     // row stride in LDS (bf16), 16-byte pad
+    constexpr int P = KT + 8;                     // B row stride in LDS (bf16), 16-byte pad
+    constexpr int PA = KT + 4;                    // A row stride in LDS (fp32), 16-byte pad
     constexpr int CPR = KT / 8;                   // 16-byte chunks per row per slice
     // chunks (VEC) or elements per thread; an A slice smaller than 256
     // chunks leaves the threads past its end idle (tiles of 8 rows)
@@ -47,11 +51,17 @@ __global__ __launch_bounds__(256) void naive_gemm_kernel(const uint16_t* __restr
     static_assert(VEC ? TN * CPR % 256 == 0 : TN * KT % 256 == 0, "B slices in whole passes");
     static_assert(VEC ? (TM * CPR % 256 == 0 || TM * CPR < 256) : (TM * KT % 256 == 0 || TM * KT < 256),
                   "A slice: whole passes or one partial pass");
-    __shared__ __attribute__((aligned(16))) uint16_t As[TM][P];
+    // A is kept as fp32 (converted once when stored; each A element feeds
+    // TN/RN threads), B as bf16 (converted at each use)
+    __shared__ __attribute__((aligned(16))) float As[TM][PA];
     __shared__ __attribute__((aligned(16))) uint16_t Bs[TN][P];
 
+    // a thread's rows are XT (YT) apart, so the lanes of a wave read
+    // consecutive LDS rows (a 16-byte-padded row stride spreads them over the
+    // banks; rows RN apart would put lanes on the same banks)
+    constexpr uint32_t XT = TN / RN, YT = TM / RM;
     const uint32_t t = threadIdx.x;
-    const uint32_t tx = t % (TN / RN), ty = t / (TN / RN);
+    const uint32_t tx = t % XT, ty = t / XT;
     const uint32_t m0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
 
     // one K slice in registers (the next is loaded while this one is used)
@@ -90,8 +100,16 @@ __global__ __launch_bounds__(256) void naive_gemm_kernel(const uint16_t* __restr
 #pragma unroll
             for (int e = 0; e < CA; ++e) {
                 const uint32_t idx = e * 256u + t;
-                if (idx < (uint32_t)(TM * CPR))
-                    *reinterpret_cast<u32x4_t*>(&As[idx / CPR][(idx % CPR) * 8]) = va[e];
+                if (idx < (uint32_t)(TM * CPR)) {
+                    const u32x4_t v = va[e];
+                    float* dst = &As[idx / CPR][(idx % CPR) * 8];
+                    *reinterpret_cast<f32x4_t*>(dst) =
+                        f32x4_t{bf16_bits_to_f32(v[0] & 0xFFFFu), bf16_bits_to_f32(v[0] >> 16),
+                                bf16_bits_to_f32(v[1] & 0xFFFFu), bf16_bits_to_f32(v[1] >> 16)};
+                    *reinterpret_cast<f32x4_t*>(dst + 4) =
+                        f32x4_t{bf16_bits_to_f32(v[2] & 0xFFFFu), bf16_bits_to_f32(v[2] >> 16),
+                                bf16_bits_to_f32(v[3] & 0xFFFFu), bf16_bits_to_f32(v[3] >> 16)};
+                }
             }
 #pragma unroll
             for (int e = 0; e < CB; ++e) {
@@ -102,7 +120,7 @@ __global__ __launch_bounds__(256) void naive_gemm_kernel(const uint16_t* __restr
 #pragma unroll
             for (int e = 0; e < LA; ++e) {
                 const uint32_t idx = e * 256u + t;
-                if (idx < (uint32_t)(TM * KT)) As[idx / KT][idx % KT] = sa[e];
+                if (idx < (uint32_t)(TM * KT)) As[idx / KT][idx % KT] = bf16_bits_to_f32(sa[e]);
             }
 #pragma unroll
             for (int e = 0; e < LB; ++e) {
@@ -118,20 +136,24 @@ __global__ __launch_bounds__(256) void naive_gemm_kernel(const uint16_t* __restr
 #pragma unroll
         for (int j = 0; j < RN; ++j) acc[i][j] = 0.f;
 
-    // 8 consecutive k of a row as one 16-byte LDS read; the 8 FMAs of a chain
-    // run in k order
+    // 8 consecutive k of a B row as one 16-byte LDS read (two for A in fp32);
+    // the 8 FMAs of a chain run in k order
     auto chunk = [&](uint32_t kk, int cnt) {
-        u32x4_t a[RM], b[RN];
+        f32x4_t a[RM][2];
+        u32x4_t b[RN];
 #pragma unroll
-        for (int i = 0; i < RM; ++i) a[i] = *reinterpret_cast<const u32x4_t*>(&As[ty * RM + i][kk]);
+        for (int i = 0; i < RM; ++i) {
+            a[i][0] = *reinterpret_cast<const f32x4_t*>(&As[ty + i * YT][kk]);
+            a[i][1] = *reinterpret_cast<const f32x4_t*>(&As[ty + i * YT][kk + 4]);
+        }
 #pragma unroll
-        for (int j = 0; j < RN; ++j) b[j] = *reinterpret_cast<const u32x4_t*>(&Bs[tx * RN + j][kk]);
+        for (int j = 0; j < RN; ++j) b[j] = *reinterpret_cast<const u32x4_t*>(&Bs[tx + j * XT][kk]);
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
             if (q < cnt) {
 #pragma unroll
                 for (int i = 0; i < RM; ++i) {
-                    const float av = bf16_bits_to_f32((a[i][q >> 1] >> (16 * (q & 1))) & 0xFFFFu);
+                    const float av = a[i][q >> 2][q & 3];
 #pragma unroll
                     for (int j = 0; j < RN; ++j) {
                         const float bv = bf16_bits_to_f32((b[j][q >> 1] >> (16 * (q & 1))) & 0xFFFFu);
@@ -157,11 +179,11 @@ __global__ __launch_bounds__(256) void naive_gemm_kernel(const uint16_t* __restr
 
 #pragma unroll
     for (int i = 0; i < RM; ++i) {
-        const uint32_t m = m0 + ty * RM + i;
+        const uint32_t m = m0 + ty + i * YT;
         if (m >= M) continue;
 #pragma unroll
         for (int j = 0; j < RN; ++j) {
-            const uint32_t n = n0 + tx * RN + j;
+            const uint32_t n = n0 + tx + j * XT;
             if (n < N) C[(size_t)m * ldc + n] = acc[i][j];
         }
     }
@@ -194,7 +216,7 @@ hipError_t launch_gemm_naive(const void* A, const void* B, float* C, uint32_t M,
     else if (M <= 16)
         launch_cfg<16, 128, 2, 4, 128>(vec, A, B, C, M, N, K, lda, ldb, ldc, st);
     else if (M <= 32)
-        launch_cfg<32, 128, 4, 4, 64>(vec, A, B, C, M, N, K, lda, ldb, ldc, st);
+        launch_cfg<32, 256, 4, 8, 64>(vec, A, B, C, M, N, K, lda, ldb, ldc, st);
     else
         launch_cfg<64, 64, 4, 4, 64>(vec, A, B, C, M, N, K, lda, ldb, ldc, st);
     return hipGetLastError();

@@ -42,7 +42,8 @@ def test_reference_test_gemm(dev):
     (37, 53, 77, 80, 100, 60),          # ragged everything, strided
     (16, 300, 96, 96, 96, 304),         # M exactly one small tile
     (70, 130, 200, 200, 256, 130),      # several tiles in both directions
-    (32, 700, 2048, 2048, 2048, 700),   # batch lm_head-like at M = 32 (32 x 128 tiles)
+    (32, 700, 2048, 2048, 2048, 700),   # batch lm_head-like at M = 32 (32 x 256 tiles)
+    (24, 1000, 512, 512, 512, 1000),    # 32-row tile, 16-byte loads, ragged N and M
     (17, 257, 100, 104, 100, 260),      # 32-row tile, ragged and strided
     (8, 600, 2048, 2048, 2048, 600),    # 8-row tile (M <= 8)
     (3, 300, 90, 96, 90, 300),          # 8-row tile, ragged K and strides (element loads)
