@@ -19,11 +19,13 @@
 // consecutive k of each of its B rows as one 16-byte LDS read (two for an A
 // row) and runs the 8 FMAs of every chain in k order. The chains
 // cannot be split over k, so the slice depth sets how many load round trips
-// a chain waits for. Tile shapes: 64 x 64 (KT 64) for general M; 8 x 256
-// (KT 64), 16 x 128 (KT 128) and 32 x 256 (KT 64) for M <= 8 / 16 / 32 (the
-// batch lm_head, where a taller tile would spend half or more of its FMAs on
-// padding rows); 16 x 16 (KT 512) for N <= 32 (gate_proj N=16). Element
-// loads (any stride) use a quarter of the slice depth.
+// a chain waits for. A thread converts RN B values per k for RM x RN FMAs,
+// so taller register tiles cost fewer conversions. Tile shapes (KT 64):
+// 64 x 64 (4 x 4 per thread) for general M; 8 x 256 (2 x 4), 16 x 256
+// (4 x 4) and 32 x 256 (8 x 4) for M <= 8 / 16 / 32 (the batch lm_head,
+// where a taller tile would spend half or more of its FMAs on padding rows);
+// 16 x 16 (1 x 1, KT 512) for N <= 32 (gate_proj N=16). Element loads (any
+// stride) use a quarter of the slice depth.
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -214,9 +216,9 @@ hipError_t launch_gemm_naive(const void* A, const void* B, float* C, uint32_t M,
     else if (M <= 8)
         launch_cfg<8, 256, 2, 4, 64>(vec, A, B, C, M, N, K, lda, ldb, ldc, st);
     else if (M <= 16)
-        launch_cfg<16, 128, 2, 4, 128>(vec, A, B, C, M, N, K, lda, ldb, ldc, st);
+        launch_cfg<16, 256, 4, 4, 64>(vec, A, B, C, M, N, K, lda, ldb, ldc, st);
     else if (M <= 32)
-        launch_cfg<32, 256, 4, 8, 64>(vec, A, B, C, M, N, K, lda, ldb, ldc, st);
+        launch_cfg<32, 256, 8, 4, 64>(vec, A, B, C, M, N, K, lda, ldb, ldc, st);
     else
         launch_cfg<64, 64, 4, 4, 64>(vec, A, B, C, M, N, K, lda, ldb, ldc, st);
     return hipGetLastError();

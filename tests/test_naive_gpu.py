@@ -38,7 +38,8 @@ def test_reference_test_gemm(dev):
 @pytest.mark.parametrize("M,N,K,lda,ldb,ldc", [
     (1, 16, 2048, 2048, 2048, 16),      # gate_proj N=16, one token
     (128, 16, 2048, 2048, 2048, 16),    # gate_proj over a 128-token prefill chunk
-    (8, 1000, 2048, 2048, 2048, 1000),  # batch lm_head-like, ragged N, M <= 16 tile
+    (8, 1000, 2048, 2048, 2048, 1000),  # batch lm_head-like, ragged N, 8-row tile
+    (12, 1000, 2048, 2048, 2048, 1000), # 16-row tile, ragged N and M
     (37, 53, 77, 80, 100, 60),          # ragged everything, strided
     (16, 300, 96, 96, 96, 304),         # M exactly one small tile
     (70, 130, 200, 200, 256, 130),      # several tiles in both directions
