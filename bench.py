@@ -1,22 +1,31 @@
 """Benchmark of the quantized-matmul hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--all] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
 
 Headline (the JSON line's `value`): the 4-bit decode GEMV at M=1, K=2048,
 N=8192, group 64, bf16 out, as HBM GB/s of algorithmic bytes
 (q + scales + biases + x + y = 9,457,664 B per launch). A step is one GEMV
-launch over one weight copy; launches rotate over enough distinct copies
-(>= 1 GiB) that the 256 MB Infinity Cache cannot hold them, so every step
-streams its weights from HBM. The K timed steps run as one HIP graph replay
-(back-to-back launches, no host in the loop), bracketed by synchronize and
-hipEvents on the launch stream.
+launch over one weight copy.
 
-`roofline` reports the same kernel's average launch duration over that
-replay (steps / event time), against the 8 TB/s HBM peak. The `gemm` object reports the
-bf16 prefill GEMM at M=1024, K=2048, N=8192 (34.36 GFLOP) against the dense
-bf16 MFMA peak. `cpu_baseline` times the CPU oracle (the reference's per-
-element dequant check loop, restated in C) on the same workload on the host.
-`--all` adds a per-config table (configs 0-4) to the JSON under "configs".
+Timing protocol (every row):
+  * launches rotate over distinct operand copies totalling >= 1 GiB;
+  * the K timed launches are captured once into a HIP graph; the graph is
+    replayed once untimed (upload), then a 1 GiB buffer is read and written
+    (evicting the 256 MB Infinity Cache and the L2s), then the timed replay
+    runs, bracketed by synchronize and hipEvents on the launch stream. Every
+    weight byte of the timed replay therefore comes from HBM, whatever K is;
+    `copies_touched` and `bytes_touched` say how much distinct weight data
+    the timed replay read;
+  * the per-launch time is the replay time / K: back-to-back launches, so it
+    includes the gap between kernels (the kernel trace in profiles/ gives
+    the kernels' own durations).
+
+The JSON line carries one row per BASELINE config (`configs`), each with
+its roofline fraction and a CPU baseline: the CPU oracle (the reference's
+per-element check loops, restated in C) timed single-threaded on a bounded
+sample of the same workload on this host, extrapolated where stated. The
+batch dispatch policy table (exact 4-bit batched GEMV vs the bf16-cache GEMM
+vs the fused 4-bit GEMM, M = 1..32, config-1 shapes) is under `policy`.
 """
 from __future__ import annotations
 
@@ -24,6 +33,7 @@ import argparse
 import json
 import math
 import os
+import platform
 import sys
 import time
 
@@ -33,10 +43,11 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 ROTATE_BYTES = 1 << 30
+FLUSH_BYTES = 1 << 30
 
 
 def measured_traffic():
-    """HBM bytes per launch of the headline GEMV, from the committed rocprofv3
+    """HBM bytes per launch of the headline GEMV from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE passes (scaled by a 256 MiB copy), or None."""
     import re
 
@@ -48,78 +59,129 @@ def measured_traffic():
     return int(m.group(1)) if m else None
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
 def _parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200)
     p.add_argument("--warmup", type=int, default=20)
-    p.add_argument("--all", action="store_true", help="also time every benchmark config")
-    p.add_argument("--config", type=int, default=None, choices=range(5),
-                   help="also time the cases of one benchmark config (0-4)")
-    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--quick", action="store_true",
+                   help="headline, GEMM and config rows only (no policy table, no chain)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     p.add_argument("--calib-copy", action="store_true",
                    help="also run a 256 MiB device copy (reference for the HBM byte counters)")
     return p.parse_args()
 
 
+def roofline(us, nbytes, flops):
+    """Roofline of one launch: the bound is whichever of HBM (algorithmic
+    bytes at 8 TB/s) and dense bf16 MFMA (flops at 2.5 PFLOP/s) takes longer."""
+    t_hbm = nbytes / (HBM_PEAK_GBS * 1e9)
+    t_mfma = flops / (BF16_PEAK_TFLOPS * 1e12)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    tfs = flops / (us * 1e-6) / 1e12
+    if t_hbm >= t_mfma:
+        return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    return {"bound": "mfma", "achieved": round(tfs, 1), "peak": BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(tfs / BF16_PEAK_TFLOPS, 4)}
+
+
 class Timer:
-    """Times a launch function over rotating operand sets.
+    """Times `steps` launches of fn(i) as one HIP-graph replay, with the
+    caches flushed between the upload replay and the timed one."""
 
-    The timed steps are captured once into a HIP graph and replayed, so the
-    launches run back to back with no host in the loop; the time is taken
-    with hipEvents recorded on the launch stream around the replay, after a
-    device synchronize. steps/time is the per-launch average duration (it
-    agrees with rocprofv3's per-kernel average; see profiles/)."""
-
-    def __init__(self, torch):
+    def __init__(self, torch, dev):
         self.torch = torch
+        self.flush = torch.zeros(FLUSH_BYTES // 4, dtype=torch.int32, device=dev)
+
+    def _flush(self):
+        self.flush.add_(1)  # reads and writes 1 GiB (about 0.3 ms)
+        self.flush.add_(1)
 
     def run(self, fn, steps, warmup):
-        """Return (total_ms for `steps` launches, mode)."""
+        """Return (ms for `steps` launches, mode)."""
         torch = self.torch
         for i in range(warmup):
             fn(i)
         torch.cuda.synchronize()
         s0 = torch.cuda.Event(enable_timing=True)
         s1 = torch.cuda.Event(enable_timing=True)
-        try:
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                for i in range(steps):
-                    fn(i)
-            g.replay()  # the first replay uploads the graph
-            torch.cuda.synchronize()
-            s0.record()
-            g.replay()
-            s1.record()
-            torch.cuda.synchronize()
-            return s0.elapsed_time(s1), "hip-graph"
-        except RuntimeError as e:
-            print(f"[bench] graph capture failed ({e}); timing eager launches", file=sys.stderr)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(steps):
+                fn(i)
+        g.replay()  # the first replay uploads the graph
         torch.cuda.synchronize()
+        # The flush is enqueued, not waited for: while the GPU works through
+        # it, the host submits the timed replay, so the host-side graph
+        # launch cost stays outside the events.
+        self._flush()
         s0.record()
-        for i in range(steps):
-            fn(i)
+        g.replay()
         s1.record()
         torch.cuda.synchronize()
-        return s0.elapsed_time(s1), "eager"
+        del g
+        return s0.elapsed_time(s1), "hip-graph, caches flushed (1 GiB) before the timed replay"
 
 
-def gemv_case(torch, ops, synth, dev, bits, M, N, K, G, out_dtype, timer, steps, warmup):
-    w = synth.quant_weights(N, K, G, bits, seed=synth.BASE_SEED + bits * 100 + M)
-    base = ops.QuantLinear(w, dev)
-    wbytes = w.nbytes
-    copies = max(1, math.ceil(ROTATE_BYTES / wbytes))
-    qs = [base.q] + [base.q.clone() for _ in range(copies - 1)]
-    ss = [base.s] + [base.s.clone() for _ in range(copies - 1)]
-    bs = [base.b] + [base.b.clone() for _ in range(copies - 1)]
-    x = ops.to_device_bits(synth.activations(M, K), dev)
-    y = torch.empty((M, N), dtype=out_dtype, device=dev)
+def _rotating(t, copies):
+    return [t] + [t.clone() for _ in range(copies - 1)]
+
+
+def _dev_quant(torch, dev, N, K, G, bits, gen):
+    """Random MLX-affine weights made on the device (the benchmark
+    distributions; a device generator, so large and many-layer cases need no
+    host generation): q uniform words, scale ~ U(lo, hi), bias = -mid*scale
+    (+ N(0, 1e-3) for 4-bit)."""
+    words = N * K * bits // 32
+    q = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, words // N), dtype=torch.int32, device=dev,
+                      generator=gen)
+    ng = K // G
     if bits == 4:
-        f1, fb = ops.gemv4, ops.gemv4_b
+        s = (0.001 + 0.009 * torch.rand(N, ng, device=dev, generator=gen)).to(torch.bfloat16)
+        b = (-8.0 * s.float() + 1e-3 * torch.randn(N, ng, device=dev, generator=gen)).to(torch.bfloat16)
     else:
-        f1, fb = ops.gemv8, ops.gemv8_b
+        s = (1e-4 + 9e-4 * torch.rand(N, ng, device=dev, generator=gen)).to(torch.bfloat16)
+        b = (-128.0 * s.float()).to(torch.bfloat16)
+    return q, s, b
+
+
+class Ctx:
+    def __init__(self, torch, ops, synth, dev, timer, steps, warmup):
+        self.torch, self.ops, self.synth, self.dev = torch, ops, synth, dev
+        self.timer, self.steps, self.warmup = timer, steps, warmup
+        self.gen = torch.Generator(device=dev)
+        self.gen.manual_seed(0x4D494F52)
+
+
+def gemv_row(c, bits, M, N, K, G=64, steps=None, hot=False, tag=None):
+    """Configs 0-2: the exact 4/8-bit GEMV (M = 1) or batched GEMV (M > 1),
+    bf16 out, on rotating weight copies."""
+    torch, ops = c.torch, c.ops
+    steps = steps or c.steps
+    if bits == 8 and N >= 65536:
+        q, s, b = _dev_quant(torch, c.dev, N, K, G, bits, c.gen)
+    else:
+        w = c.synth.quant_weights(N, K, G, bits, seed=c.synth.BASE_SEED + bits * 100 + M)
+        lin = ops.QuantLinear(w, c.dev)
+        q, s, b = lin.q, lin.s, lin.b
+    wbytes = q.numel() * 4 + s.numel() * 2 + b.numel() * 2
+    copies = max(1, math.ceil(ROTATE_BYTES / wbytes))
+    qs, ss, bs = _rotating(q, copies), _rotating(s, copies), _rotating(b, copies)
+    x = ops.to_device_bits(c.synth.activations(M, K), c.dev)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=c.dev)
+    f1 = ops.gemv4 if bits == 4 else ops.gemv8
+    fb = ops.gemv4_b if bits == 4 else ops.gemv8_b
 
     def fn(i):
         j = i % copies
@@ -128,78 +190,62 @@ def gemv_case(torch, ops, synth, dev, bits, M, N, K, G, out_dtype, timer, steps,
         else:
             fb(qs[j], ss[j], bs[j], x, y, N, K, M, group=G)
 
-    # The same launches on one weight copy, served from the 256 MB Infinity
-    # Cache once warm: reported under its own label, never as the headline.
-    # Timed first, so the rotating (HBM) launches are the last in a trace.
-    hot = None
-    if copies > 1 and wbytes < 128 * 1024 * 1024:
-        hot, _ = timer.run(lambda i: fn(0), steps, warmup)
-    total, mode = timer.run(fn, steps, warmup)
-    per = total / steps
-    ybytes = M * N * (2 if out_dtype == torch.bfloat16 else 4)
-    algo = wbytes + M * K * 2 + ybytes
+    total, mode = c.timer.run(fn, steps, c.warmup)
+    us = total * 1e3 / steps
+    nbytes = wbytes + M * K * 2 + M * N * 2
     flops = 2.0 * M * N * K
-    res = dict(M=M, N=N, K=K, G=G, bits=bits, bytes=algo, copies=copies, mode=mode,
-               us_per_step=total * 1e3 / steps, us_kernel=per * 1e3,
-               gbs_step=algo * steps / (total * 1e-3) / 1e9,
-               gbs_kernel=algo / (per * 1e-3) / 1e9,
-               tflops_kernel=flops / (per * 1e-3) / 1e12)
-    res["hbm_frac_kernel"] = res["gbs_kernel"] / HBM_PEAK_GBS
-    if hot is not None:
-        res["us_hot_cache"] = hot * 1e3 / steps
-        res["gbs_hot_cache"] = algo / (hot / steps * 1e-3) / 1e9
-    del qs, ss, bs, base
+    row = dict(name=tag or f"gemv{bits}" + ("" if M == 1 else "_b"), M=M, N=N, K=K, G=G,
+               us=round(us, 3), GB_s=round(nbytes / (us * 1e-6) / 1e9, 1),
+               TFLOP_s=round(flops / (us * 1e-6) / 1e12, 2), bytes=nbytes, flops=flops,
+               roofline=roofline(us, nbytes, flops), steps=steps, copies=copies,
+               copies_touched=min(steps, copies), bytes_touched=steps * wbytes, timing=mode)
+    if hot:
+        th, _ = c.timer.run(lambda i: fn(0), steps, c.warmup)
+        row["hot_cache_us"] = round(th * 1e3 / steps, 3)
+    del qs, ss, bs
     torch.cuda.empty_cache()
-    return res
+    return row
 
 
-def gemm_case(torch, ops, synth, oracle_mod, dev, M, N, K, fused, timer, steps, warmup, G=64,
-              vendor=False):
-    w = synth.quant_weights(N, K, G, 4, seed=synth.BASE_SEED + N + K)
-    lin = ops.QuantLinear(w, dev)
-    A = ops.to_device_bits(synth.activations(M, K), dev)
-    C = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+def gemm_row(c, M, N, K, fused, steps=30, vendor=False, G=64):
+    """Config 3 (bf16 weight cache) or config 4 (fused 4-bit), bf16 out."""
+    torch, ops = c.torch, c.ops
+    q, s, b = _dev_quant(torch, c.dev, N, K, G, 4, c.gen)
+    A = ops.to_device_bits(c.synth.activations(M, K), c.dev)
+    C = torch.empty((M, N), dtype=torch.bfloat16, device=c.dev)
     if fused:
-        wbytes = w.nbytes
+        wbytes = q.numel() * 4 + s.numel() * 2 + b.numel() * 2
         copies = max(1, math.ceil(ROTATE_BYTES / wbytes))
-        qs = [lin.q] + [lin.q.clone() for _ in range(copies - 1)]
-        ss = [lin.s] + [lin.s.clone() for _ in range(copies - 1)]
-        bs = [lin.b] + [lin.b.clone() for _ in range(copies - 1)]
+        qs, ss, bs = _rotating(q, copies), _rotating(s, copies), _rotating(b, copies)
 
         def fn(i):
             j = i % copies
             ops.gemm_q4(A, qs[j], ss[j], bs[j], C, M, N, K, group=G)
     else:
-        Bd = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
-        ops.dequant_tile(lin.q, lin.s, lin.b, Bd, N, K, group=G)
+        Bd = torch.empty((N, K), dtype=torch.bfloat16, device=c.dev)
+        ops.dequant_tile(q, s, b, Bd, N, K, group=G)
         wbytes = N * K * 2
         copies = max(1, math.ceil(ROTATE_BYTES / wbytes))
-        Bs = [Bd] + [Bd.clone() for _ in range(copies - 1)]
+        Bs = _rotating(Bd, copies)
 
         def fn(i):
             ops.gemm_mpp(A, Bs[i % copies], C, M, N, K)
 
-    total, mode = timer.run(fn, steps, warmup)
-    per = total / steps
+    total, mode = c.timer.run(fn, steps, min(c.warmup, 5))
+    us = total * 1e3 / steps
     flops = 2.0 * M * N * K
-    algo = wbytes + M * K * 2 + M * N * 2
-    vendor_us = None
+    nbytes = wbytes + M * K * 2 + M * N * 2
+    row = dict(name="gemm_q4_fused" if fused else "gemm_bf16", M=M, N=N, K=K,
+               us=round(us, 2), TFLOP_s=round(flops / (us * 1e-6) / 1e12, 1),
+               GB_s=round(nbytes / (us * 1e-6) / 1e9, 1), flops=flops, bytes=nbytes,
+               roofline=roofline(us, nbytes, flops), steps=steps, copies=copies,
+               copies_touched=min(steps, copies), bytes_touched=steps * wbytes, timing=mode)
     if vendor and not fused:
-        # the vendor GEMM (torch.matmul -> hipBLASLt) on the same operands and rotation
-        vt, _ = timer.run(lambda i: torch.matmul(A, Bs[i % copies].t(), out=C), steps, warmup)
-        vendor_us = vt * 1e3 / steps
-    res = dict(M=M, N=N, K=K, fused=fused, copies=copies, mode=mode,
-               us_per_step=total * 1e3 / steps, us_kernel=per * 1e3,
-               tflops_kernel=flops / (per * 1e-3) / 1e12,
-               tflops_step=flops * steps / (total * 1e-3) / 1e12,
-               gbs_kernel=algo / (per * 1e-3) / 1e9)
-    res["mfma_frac_kernel"] = res["tflops_kernel"] / BF16_PEAK_TFLOPS
-    if vendor_us is not None:
-        res["vendor_us"] = vendor_us
-        res["vendor_tflops"] = flops / (vendor_us * 1e-6) / 1e12
-    res["hbm_frac_kernel"] = res["gbs_kernel"] / HBM_PEAK_GBS
+        vt, _ = c.timer.run(lambda i: torch.matmul(A, Bs[i % copies].t(), out=C), steps, 5)
+        row["hipblaslt_us"] = round(vt * 1e3 / steps, 2)
+        row["hipblaslt_TFLOP_s"] = round(flops / (vt * 1e-3 / steps) / 1e12, 1)
     torch.cuda.empty_cache()
-    return res
+    return row
 
 
 # One LFM-style layer's projections (name, K, N), BASELINE config 4.
@@ -207,280 +253,320 @@ LAYER = [("q", 2048, 2048), ("k", 2048, 512), ("v", 2048, 512), ("o", 2048, 2048
          ("gate", 2048, 8192), ("up", 2048, 8192), ("down", 8192, 2048)]
 
 
-class _Stacked:
-    """Row-stacked weights of projections that read the same activation
-    (q|k|v, gate|up): one product of N = sum of the parts, the same values
-    per output row as the separate products."""
-
-    def __init__(self, torch, lins):
-        self.q = torch.cat([l.q for l in lins], 0)
-        self.s = torch.cat([l.s for l in lins], 0)
-        self.b = torch.cat([l.b for l in lins], 0)
-
-
-def chain_case(torch, ops, synth, dev, M, timer, layers=24, G=64, steps=3, warmup=1,
-               stacked=False):
+def chain_row(c, M, stacked, layers=24, G=64, steps=3):
     """Config 4: the fused 4-bit GEMM over a synthetic 24-layer projection
-    chain (7 projections per layer, distinct random weights per layer), M
-    activation rows. One step = the whole chain: 168 GEMMs, or with
-    `stacked` 96, q|k|v and gate|up each one product on row-stacked weights
-    (they read the same activation), as an engine lays them out."""
+    chain (7 projections per layer, distinct random weights per layer). One
+    step = the whole chain: 168 GEMMs, or with `stacked` 96, where q|k|v and
+    gate|up (which read the same activation) are each one product over
+    row-stacked weights. The 821 MB of weights exceed the Infinity Cache."""
+    torch, ops = c.torch, c.ops
     ws = []
-    for l in range(layers):
-        lins = []
-        for i, (name, K, N) in enumerate(LAYER):
-            w = synth.quant_weights(N, K, G, 4, seed=synth.BASE_SEED + 1000 * l + i)
-            lins.append((ops.QuantLinear(w, dev), K, N))
+    for _ in range(layers):
+        parts = [(_dev_quant(torch, c.dev, N, K, G, 4, c.gen), K, N) for _, K, N in LAYER]
         if stacked:
-            ws.append((_Stacked(torch, [x[0] for x in lins[0:3]]), 2048, 3072))
-            ws.append(lins[3])
-            ws.append((_Stacked(torch, [x[0] for x in lins[4:6]]), 2048, 16384))
-            ws.append(lins[6])
-            del lins
+            def cat(ps):
+                return tuple(torch.cat([p[0][i] for p in ps], 0) for i in range(3))
+            ws += [(cat(parts[0:3]), 2048, 3072), parts[3], (cat(parts[4:6]), 2048, 16384),
+                   parts[6]]
         else:
-            ws.extend(lins)
-    a2 = ops.to_device_bits(synth.activations(M, 2048), dev)
-    a8 = ops.to_device_bits(synth.activations(M, 8192), dev)
-    outs = {N: torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            ws += parts
+    a2 = ops.to_device_bits(c.synth.activations(M, 2048), c.dev)
+    a8 = ops.to_device_bits(c.synth.activations(M, 8192), c.dev)
+    outs = {N: torch.empty((M, N), dtype=torch.bfloat16, device=c.dev)
             for N in (512, 2048, 3072, 8192, 16384)}
 
     def fn(i):
-        for lin, K, N in ws:
-            ops.gemm_q4(a8 if K == 8192 else a2, lin.q, lin.s, lin.b, outs[N], M, N, K, group=G)
+        for (q, s, b), K, N in ws:
+            ops.gemm_q4(a8 if K == 8192 else a2, q, s, b, outs[N], M, N, K, group=G)
 
-    total, mode = timer.run(fn, steps, warmup)
-    per = total / steps
+    total, mode = c.timer.run(fn, steps, 1)
+    us = total * 1e3 / steps
     flops = sum(2.0 * M * N * K for _, K, N in ws)
-    wbytes = sum(l.q.numel() * 4 + l.s.numel() * 2 + l.b.numel() * 2 for l, _, _ in ws)
-    res = dict(config=4, M=M, layers=layers, gemms=len(ws), stacked=stacked, mode=mode,
-               us_per_chain=per * 1e3,
-               tflops=flops / (per * 1e-3) / 1e12, weight_gbs=wbytes / (per * 1e-3) / 1e9,
-               weight_bytes=wbytes, flops=flops)
-    res["mfma_frac"] = res["tflops"] / BF16_PEAK_TFLOPS
-    res["hbm_frac"] = res["weight_gbs"] / HBM_PEAK_GBS
+    wbytes = sum(q.numel() * 4 + s.numel() * 2 + b.numel() * 2 for (q, s, b), _, _ in ws)
+    nbytes = wbytes + sum(M * K * 2 + M * N * 2 for _, K, N in ws)
+    row = dict(name="chain_q4_fused" + ("_stacked" if stacked else ""), M=M, layers=layers,
+               gemms=len(ws), us=round(us, 1), TFLOP_s=round(flops / (us * 1e-6) / 1e12, 1),
+               weight_GB_s=round(wbytes / (us * 1e-6) / 1e9, 1), flops=flops, bytes=nbytes,
+               roofline=roofline(us, nbytes, flops), steps=steps, bytes_touched=steps * wbytes,
+               timing=mode)
     del ws
     torch.cuda.empty_cache()
-    return res
+    return row
 
 
-def fused_decode_case(torch, ops, synth, dev, N, K, timer, steps, warmup, G=64):
-    """Fused decode steps (rmsnorm -> gemv4 and silu_mul -> gemv4, as the
-    reference's engine.cpp:388-400 runs them in two launches) against the
-    plain gemv4 on the same rotating weights: the fused launch reads the fp32
-    input (and the bf16 norm weight) instead of a bf16 activation."""
-    w = synth.quant_weights(N, K, G, 4, seed=synth.BASE_SEED + 7 * N + K)
-    base = ops.QuantLinear(w, dev)
-    copies = max(1, math.ceil(ROTATE_BYTES / w.nbytes))
-    qs = [base.q] + [base.q.clone() for _ in range(copies - 1)]
-    ss = [base.s] + [base.s.clone() for _ in range(copies - 1)]
-    bs = [base.b] + [base.b.clone() for _ in range(copies - 1)]
-    xb = ops.to_device_bits(synth.activations(1, K), dev)
-    xf = torch.randn(K, device=dev)
-    up = torch.randn(K, device=dev)
-    nw = (torch.rand(K, device=dev) + 0.5).to(torch.bfloat16)
-    y = torch.empty(N, dtype=torch.bfloat16, device=dev)
-    res = dict(N=N, K=K, G=G, copies=copies)
-    cases = {
-        "gemv4": (lambda j: ops.gemv4(qs[j], ss[j], bs[j], xb, y, N, K, group=G), K * 2),
-        "rmsnorm_gemv4": (lambda j: ops.rmsnorm_gemv4(xf, nw, qs[j], ss[j], bs[j], y, N, K,
-                                                      group=G), K * 6),
-        "silu_mul_gemv4": (lambda j: ops.silu_mul_gemv4(xf, up, qs[j], ss[j], bs[j], y, N, K,
-                                                        group=G), K * 8),
-    }
-    for name, (f, xbytes) in cases.items():
-        total, mode = timer.run(lambda i: f(i % copies), steps, warmup)
-        per = total / steps
-        res[name + "_us"] = per * 1e3
-        res[name + "_gbs"] = (w.nbytes + xbytes + N * 2) / (per * 1e-3) / 1e9
-    res["mode"] = mode
-    del qs, ss, bs, base
+def policy_table(c, steps=50):
+    """Batch dispatch policy (BatchEngine::linear, src/batch.cpp:223-230):
+    per config-1 shape and M = 1..32, µs of the exact 4-bit batched GEMV
+    (what miori_linear_q4 runs), of the bf16-cache GEMM the reference runs
+    above 4 slots, and of the fused 4-bit GEMM, all on rotating weights."""
+    torch, ops = c.torch, c.ops
+    out = []
+    for K, N in [(2048, 2048), (2048, 512), (2048, 8192), (8192, 2048)]:
+        q, s, b = _dev_quant(torch, c.dev, N, K, 64, 4, c.gen)
+        w4 = q.numel() * 4 + s.numel() * 2 + b.numel() * 2
+        c4 = max(1, math.ceil(ROTATE_BYTES / w4))
+        qs, ss, bs = _rotating(q, c4), _rotating(s, c4), _rotating(b, c4)
+        Bd = torch.empty((N, K), dtype=torch.bfloat16, device=c.dev)
+        ops.dequant_tile(q, s, b, Bd, N, K)
+        cb = max(1, math.ceil(ROTATE_BYTES / (N * K * 2)))
+        Bs = _rotating(Bd, cb)
+        x = ops.to_device_bits(c.synth.activations(32, K), c.dev)
+        y = torch.empty((32, N), dtype=torch.bfloat16, device=c.dev)
+        rec = {"K": K, "N": N, "M": [], "exact_us": [], "bf16_cache_us": [], "fused_us": []}
+        for M in range(1, 33):
+            xm, ym = x[:M], y[:M]
+            te, _ = c.timer.run(lambda i: ops.linear(xm, qs[i % c4], ss[i % c4], bs[i % c4], ym,
+                                                     M, N, K), steps, 3)
+            tc, _ = c.timer.run(lambda i: ops.gemm_mpp(xm, Bs[i % cb], ym, M, N, K), steps, 3)
+            tf, _ = c.timer.run(lambda i: ops.gemm_q4(xm, qs[i % c4], ss[i % c4], bs[i % c4], ym,
+                                                      M, N, K), steps, 3)
+            rec["M"].append(M)
+            rec["exact_us"].append(round(te * 1e3 / steps, 2))
+            rec["bf16_cache_us"].append(round(tc * 1e3 / steps, 2))
+            rec["fused_us"].append(round(tf * 1e3 / steps, 2))
+        rec["exact_fastest_at_every_M"] = all(
+            e <= min(cc, f) * 1.02 for e, cc, f in zip(rec["exact_us"], rec["bf16_cache_us"],
+                                                         rec["fused_us"]))
+        out.append(rec)
+        print(f"[bench] policy {rec}", file=sys.stderr, flush=True)
+        del qs, ss, bs, Bs
+        torch.cuda.empty_cache()
+    return out
+
+
+def fused_decode_row(c, N, K, steps=100, G=64):
+    """Fused decode steps (rmsnorm -> gemv4 and silu_mul -> gemv4, which the
+    reference's engine.cpp:388-400 runs as two launches) against the plain
+    gemv4 on the same rotating weights."""
+    torch, ops = c.torch, c.ops
+    q, s, b = _dev_quant(torch, c.dev, N, K, G, 4, c.gen)
+    wbytes = q.numel() * 4 + s.numel() * 2 + b.numel() * 2
+    copies = max(1, math.ceil(ROTATE_BYTES / wbytes))
+    qs, ss, bs = _rotating(q, copies), _rotating(s, copies), _rotating(b, copies)
+    xb = ops.to_device_bits(c.synth.activations(1, K), c.dev)
+    xf = torch.randn(K, device=c.dev)
+    up = torch.randn(K, device=c.dev)
+    nw = (torch.rand(K, device=c.dev) + 0.5).to(torch.bfloat16)
+    y = torch.empty(N, dtype=torch.bfloat16, device=c.dev)
+    row = dict(name="fused_decode", N=N, K=K, G=G)
+    for name, f in {
+        "gemv4": lambda j: ops.gemv4(qs[j], ss[j], bs[j], xb, y, N, K, group=G),
+        "rmsnorm_gemv4": lambda j: ops.rmsnorm_gemv4(xf, nw, qs[j], ss[j], bs[j], y, N, K, group=G),
+        "silu_mul_gemv4": lambda j: ops.silu_mul_gemv4(xf, up, qs[j], ss[j], bs[j], y, N, K,
+                                                       group=G),
+    }.items():
+        t, _ = c.timer.run(lambda i: f(i % copies), steps, 5)
+        row[name + "_us"] = round(t * 1e3 / steps, 3)
+    del qs, ss, bs
     torch.cuda.empty_cache()
-    return res
+    return row
 
 
-def naive_case(torch, ops, dev, M, N, K, timer, steps, warmup):
-    """gemm_naive, the any-shape fallback: C fp32 [M][N] = A [M][K] . B [N][K]^T,
-    bf16 operands (the N=16 gate_proj and the bf16 batch lm_head)."""
-    A = torch.randn(M, K, device=dev).to(torch.bfloat16)
-    B = torch.randn(N, K, device=dev).to(torch.bfloat16)
-    C = torch.empty(M, N, dtype=torch.float32, device=dev)
-    total, mode = timer.run(lambda i: ops.gemm_naive(A, B, C, M, N, K, K, K, N), steps, warmup)
-    per = total / steps
-    algo = (M * K + N * K) * 2 + M * N * 4
-    return dict(M=M, N=N, K=K, mode=mode, us_kernel=per * 1e3,
-                gbs_kernel=algo / (per * 1e-3) / 1e9,
-                tflops_kernel=2.0 * M * N * K / (per * 1e-3) / 1e12)
+def naive_row(c, M, N, K, steps=20):
+    """gemm_naive, the any-shape fallback (bf16 operands, fp32 C)."""
+    torch, ops = c.torch, c.ops
+    A = torch.randn(M, K, device=c.dev).to(torch.bfloat16)
+    B = torch.randn(N, K, device=c.dev).to(torch.bfloat16)
+    C = torch.empty(M, N, dtype=torch.float32, device=c.dev)
+    t, _ = c.timer.run(lambda i: ops.gemm_naive(A, B, C, M, N, K, K, K, N), steps, 3)
+    us = t * 1e3 / steps
+    return dict(name="gemm_naive", M=M, N=N, K=K, us=round(us, 2),
+                TFLOP_s=round(2.0 * M * N * K / (us * 1e-6) / 1e12, 1))
 
 
-def calib_copy(torch, dev):
-    """A plain 256 MiB device copy: reads and writes exactly 256 MiB, the
-    reference for scaling FETCH_SIZE / WRITE_SIZE counters to bytes."""
-    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
-    dst = torch.empty_like(src)
-    for _ in range(3):
-        dst.copy_(src)
-    torch.cuda.synchronize()
-
-
-def launch_floors(torch, dev, timer, nbytes, steps):
-    """What one launch of this size costs in vendor kernels on the same box,
-    timed like the GEMV (HIP-graph replay, operands rotating over >= 1 GiB):
-    an empty launch (a 1-element fill), and torch's device copy moving the
-    same number of bytes (half read, half written)."""
-    tiny = torch.empty(1, device=dev)
-    t_fill, _ = timer.run(lambda i: tiny.zero_(), steps, 10)
+def launch_floors(c, nbytes, steps):
+    """Vendor kernels timed like the GEMV on the same box: an empty launch
+    (a 1-element fill) and torch's device copy moving the GEMV's bytes (half
+    read, half written), sources rotating over >= 1 GiB."""
+    torch = c.torch
+    tiny = torch.empty(1, device=c.dev)
+    t_fill, _ = c.timer.run(lambda i: tiny.zero_(), steps, 10)
     half = nbytes // 2 // 4
     copies = math.ceil(ROTATE_BYTES / (half * 4))
-    srcs = [torch.empty(half, dtype=torch.int32, device=dev) for _ in range(copies)]
-    dst = torch.empty(half, dtype=torch.int32, device=dev)
-    t_copy, _ = timer.run(lambda i: dst.copy_(srcs[i % copies]), steps, 10)
+    srcs = [torch.empty(half, dtype=torch.int32, device=c.dev) for _ in range(copies)]
+    dst = torch.empty(half, dtype=torch.int32, device=c.dev)
+    t_copy, _ = c.timer.run(lambda i: dst.copy_(srcs[i % copies]), steps, 10)
     del srcs
     torch.cuda.empty_cache()
     return {"empty_launch_us": round(t_fill * 1e3 / steps, 3),
-            "torch_copy_same_bytes_us": round(t_copy * 1e3 / steps, 3),
-            "note": "vendor-kernel floors for one launch moving the GEMV's bytes"}
+            "torch_copy_same_bytes_us": round(t_copy * 1e3 / steps, 3)}
 
 
-def cpu_baseline(seconds):
-    """The oracle's faithful per-element GEMV (src/main.cpp:73-84 restated)
-    on the headline workload, single-threaded, repeated for ~`seconds`."""
-    import oracle
-    from miori_amd import synth
-
-    N, K, G = 8192, 2048, 64
-    w = synth.quant_weights(N, K, G, 4, seed=synth.BASE_SEED + 400 + 1)
-    x = synth.activations(1, K)
-    algo = w.nbytes + K * 2 + N * 2
-    oracle.gemv_f64(w.q, w.s, w.b, x, 4, K, G, nthreads=1)  # warm
+# ---------------------------------------------------------------- CPU baselines
+def _timed(fn, budget):
+    """Run fn() at least once and until `budget` seconds; seconds per call."""
+    fn()  # warm
     t0 = time.perf_counter()
-    reps = 0
+    n = 0
     while True:
-        oracle.gemv_f64(w.q, w.s, w.b, x, 4, K, G, nthreads=1)
-        reps += 1
+        fn()
+        n += 1
         el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    per = el / reps
-    nt = min(16, os.cpu_count() or 1)
-    t1 = time.perf_counter()
-    oracle.gemv_f64(w.q, w.s, w.b, x, 4, K, G, nthreads=nt)
-    per_mt = time.perf_counter() - t1
-    return {"value": algo / per / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{reps} full passes of the 8192x2048 g64 4-bit GEMV (M=1), "
-                      f"per-element dequant + fp64 accumulate, {per * 1e3:.1f} ms/pass",
-            "threaded": {"value": algo / per_mt / 1e9, "cores": nt,
-                         "sample": f"1 pass with OpenMP over {nt} threads, {per_mt * 1e3:.1f} ms"}}
+        if el >= budget:
+            return el / n, n
+
+
+def cpu_baselines(synth, budget=2.5):
+    """The oracle, single-threaded, on a bounded sample of each config's
+    workload, scaled to the GPU row's unit. Returns {config: baseline}."""
+    import numpy as np
+
+    import oracle
+
+    out = {}
+    # config 0: full 8192 x 2048 g64 4-bit GEMV, M = 1 (src/main.cpp:73-84)
+    w = synth.quant_weights(8192, 2048, 64, 4, seed=synth.BASE_SEED + 401)
+    x = synth.activations(1, 2048)
+    per, n = _timed(lambda: oracle.gemv_f64(w.q, w.s, w.b, x, 4, 2048, 64, nthreads=1), budget * 2)
+    out[0] = {"value": round((w.nbytes + 4096 + 16384) / per / 1e9, 4), "unit": "GB/s",
+              "cores": 1, "kind": "port", "us": round(per * 1e6, 1),
+              "sample": f"{n} full passes of the 8192x2048 g64 4-bit GEMV (M=1), per-element "
+                        f"dequant + fp64 accumulate, {per * 1e3:.1f} ms/pass"}
+    # config 1: gate/up 2048 -> 8192 at M = 8, rows [0, 1024) extrapolated to 8192
+    x8 = synth.activations(8, 2048)
+    per, n = _timed(lambda: oracle.gemv_rows_f64(w.q, w.s, w.b, x8, 4, 2048, 64, 0, 1024), budget)
+    full = per * 8
+    nb = w.nbytes + 8 * 4096 + 8 * 8192 * 2
+    out[1] = {"value": round(nb / full / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+              "us": round(full * 1e6, 1),
+              "sample": f"{n} passes over output rows 0..1023 of the 2048->8192 g64 GEMV at "
+                        f"M=8, {per * 1e3:.1f} ms each, x8 extrapolated to all 8192 rows"}
+    # config 2: 8-bit lm_head M = 1, rows [0, 2048) extrapolated to 131072
+    w8 = synth.quant_weights(2048, 2048, 64, 8, seed=synth.BASE_SEED + 402)
+    per, n = _timed(lambda: oracle.gemv_f64(w8.q, w8.s, w8.b, x, 8, 2048, 64, nthreads=1), budget)
+    full = per * 64
+    nb = 131072 * (2048 + 2 * 32 * 2) + 4096 + 131072 * 2
+    out[2] = {"value": round(nb / full / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+              "us": round(full * 1e6, 1),
+              "sample": f"{n} passes of a 2048-row slice of the 8-bit g64 lm_head (M=1), "
+                        f"{per * 1e3:.1f} ms each, x64 extrapolated to 131072 rows"}
+    # configs 3 / 4: M=1024, K=2048, N=8192; 16 rows of A, extrapolated to 1024
+    A = synth.activations(16, 2048)
+    Bq = synth.quant_weights(8192, 2048, 64, 4, seed=synth.BASE_SEED + 403)
+    Bb = oracle.dequant_bf16(Bq.q, Bq.s, Bq.b, 4, 2048, 64)
+    rows = np.arange(16, dtype=np.int64)
+    per, n = _timed(lambda: oracle.gemm_bf16_f64(A, Bb, rows, nthreads=1), budget)
+    full = per * 64
+    flops = 2.0 * 1024 * 8192 * 2048
+    out[3] = {"value": round(flops / full / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
+              "kind": "port", "us": round(full * 1e6, 1),
+              "sample": f"{n} passes of 16 rows x 8192 x 2048 (src/main.cpp:594-601 loop, "
+                        f"fp64 accumulate), {per * 1e3:.0f} ms each, x64 extrapolated to M=1024"}
+    per_d, nd = _timed(lambda: oracle.dequant_bf16(Bq.q, Bq.s, Bq.b, 4, 2048, 64), budget / 2)
+    full4 = per_d + per * 64
+    out[4] = {"value": round(flops / full4 / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
+              "kind": "port", "us": round(full4 * 1e6, 1),
+              "sample": f"dequant of the 8192x2048 g64 weights ({per_d * 1e3:.0f} ms, {nd} "
+                        f"passes) + the config-3 GEMM sample above, for one M=1024 projection"}
+    return out
 
 
 def main():
     args = _parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
-              "the multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
+              "multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
         sys.exit(2)
     import torch
 
-    import oracle
     from miori_amd import _lib, ops, synth
 
     _lib.load()
     dev = torch.device("cuda:0")
-    timer = Timer(torch)
-    steps, warmup = args.steps, args.warmup
+    c = Ctx(torch, ops, synth, dev, Timer(torch, dev), args.steps, args.warmup)
+    t_start = time.time()
 
-    head = gemv_case(torch, ops, synth, dev, 4, 1, 8192, 2048, 64, torch.bfloat16,
-                     timer, steps, warmup)
-    gemm = gemm_case(torch, ops, synth, oracle, dev, 1024, 8192, 2048, False, timer,
-                     min(steps, 100), min(warmup, 10), vendor=True)
-    floors = launch_floors(torch, dev, timer, head["bytes"], steps)
+    def log(row):
+        print(f"[bench] {row}", file=sys.stderr, flush=True)
+        return row
 
+    head = log(gemv_row(c, 4, 1, 8192, 2048, hot=True, tag="gemv4"))
+    gemm = log(gemm_row(c, 1024, 8192, 2048, False, steps=min(args.steps, 100), vendor=True))
+    floors = launch_floors(c, head["bytes"], args.steps)
+
+    rows = [dict(config=0, **head)]
+    for K, N in [(2048, 8192), (2048, 2048), (2048, 512), (8192, 2048)]:
+        for M in (2, 4, 8, 16, 32):
+            rows.append(log(dict(config=1, **gemv_row(c, 4, M, N, K, steps=100))))
+    for M in (1, 8, 32):
+        rows.append(log(dict(config=2, **gemv_row(c, 8, M, 131072, 2048, steps=20,
+                                                  tag="gemv8_lm_head"))))
+    for fused in (False, True):
+        for M in (256, 1024, 1472):
+            for K, N in [(2048, 8192), (8192, 2048), (2048, 2560)]:
+                rows.append(log(dict(config=4 if fused else 3,
+                                     **gemm_row(c, M, N, K, fused, vendor=not fused))))
+    extra = {}
+    if not args.quick:
+        for M in (1024, 32):
+            for stacked in (False, True):
+                rows.append(log(dict(config=4, **chain_row(c, M, stacked))))
+        extra["policy"] = policy_table(c)
+        nxt = []
+        for K, N in [(2048, 2048), (2048, 8192), (8192, 2048)]:
+            nxt.append(log(fused_decode_row(c, N, K)))
+        for M, N, K in [(1, 16, 2048), (32, 16, 2048), (8, 131072, 2048), (32, 131072, 2048)]:
+            nxt.append(log(naive_row(c, M, N, K)))
+        extra["next_rows"] = nxt
+
+    cpu = None if args.no_cpu else cpu_baselines(synth)
+    if cpu:
+        for r in rows:
+            base = cpu.get(r["config"])
+            if base is None:
+                continue
+            same = ((r["config"] == 0) or (r["config"] == 1 and r["M"] == 8 and r["N"] == 8192
+                                           and r["K"] == 2048)
+                    or (r["config"] == 2 and r["M"] == 1)
+                    or (r["config"] in (3, 4) and r.get("name", "").startswith("gemm")
+                        and (r["M"], r["N"], r["K"]) == (1024, 8192, 2048)))
+            if same:
+                r["cpu_baseline"] = base
+    if args.calib_copy:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+
+    wbytes_head = head["bytes"] - 2048 * 2 - 8192 * 2
     out = {
         "metric": "4-bit GEMV HBM GB/s (% of 8 TB/s) at M=1; prefill GEMM TFLOP/s at M=1024",
-        "value": round(head["gbs_step"], 1),
+        "value": head["GB_s"],
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": steps,
-        "warmup": warmup,
-        "ms_per_step": head["us_per_step"] / 1e3,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["us"] / 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded splitmix64; MLX-affine 4-bit, group 64)",
-        "config": {"workload": "gemv4 M=1 K=2048 N=8192 group=64 bf16-out, "
-                               f"rotating {head['copies']} weight copies (HBM, not cache)",
-                   "M": 1, "N": 8192, "K": 2048, "group": 64, "timing": head["mode"]},
-        "roofline": {"bound": "hbm", "achieved": round(head["gbs_kernel"], 1),
-                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(head["gbs_kernel"] / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(), "kernel_us": round(head["us_kernel"], 3),
-                     "algorithmic_bytes": head["bytes"]},
-        "gemm": {"workload": "bf16 GEMM M=1024 K=2048 N=8192, bf16 out",
-                 "tflops": round(gemm["tflops_kernel"], 1),
-                 "us": round(gemm["us_kernel"], 2),
-                 "frac_of_bf16_peak": round(gemm["mfma_frac_kernel"], 4),
-                 "hipblaslt_us_same_operands": round(gemm["vendor_us"], 2),
-                 "hipblaslt_tflops": round(gemm["vendor_tflops"], 1)},
+        "dtype": "u4 codes, bf16 scale/bias/x, fp32 accumulate, bf16 out",
+        "data": "synthetic (seeded splitmix64 / device RNG; MLX-affine, group 64)",
+        "config": {"workload": "gemv4 M=1 K=2048 N=8192 group=64 bf16-out (BASELINE config 0)",
+                   "M": 1, "N": 8192, "K": 2048, "group": 64, "timing": head["timing"],
+                   "copies": head["copies"], "copies_touched": head["copies_touched"],
+                   "bytes_touched": head["bytes_touched"], "flush_bytes": FLUSH_BYTES,
+                   "weight_bytes_per_copy": wbytes_head},
+        "roofline": {**head["roofline"], "traffic": measured_traffic(),
+                     "traffic_source": "profiles/gemv4_k2048_n8192_hbm_traffic.md (rocprofv3 "
+                                       "FETCH_SIZE + WRITE_SIZE, scaled by a 256 MiB copy)",
+                     "launch_us": head["us"], "algorithmic_bytes": head["bytes"]},
+        "gemm": {"workload": "bf16 GEMM M=1024 K=2048 N=8192, bf16 out (config 3)",
+                 "us": gemm["us"], "TFLOP_s": gemm["TFLOP_s"], "roofline": gemm["roofline"],
+                 "hipblaslt_us": gemm["hipblaslt_us"],
+                 "hipblaslt_TFLOP_s": gemm["hipblaslt_TFLOP_s"]},
         "gemv_floors": floors,
-        "gemv_hot_cache": {"us": round(head["us_hot_cache"], 3),
-                           "gbs": round(head["gbs_hot_cache"], 1),
-                           "note": "same launches on one weight copy (Infinity Cache "
-                                   "resident); not the headline value"},
+        "gemv_hot_cache_us": head["hot_cache_us"],
+        "configs": rows,
+        **extra,
     }
-    if args.calib_copy:
-        calib_copy(torch, dev)
-    if args.all or args.config is not None:
-        out["configs"] = run_all(torch, ops, synth, oracle, dev, timer,
-                                 only=None if args.all else args.config)
-    if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    if cpu:
+        out["cpu_baseline"] = cpu[0]
+        out["cpu_model"] = cpu_model()
+        out["cpu_threads_available"] = os.cpu_count()
+    out["bench_wall_s"] = round(time.time() - t_start, 1)
     print(json.dumps(out), flush=True)
-
-
-def run_all(torch, ops, synth, oracle, dev, timer, only=None):
-    """Every benchmark config, or only config `only` (0-4; the next-row cases,
-    fused decode and gemm_naive, run with the full set)."""
-    rows = []
-    st, wu = 100, 10
-
-    def want(c):
-        return only is None or only == c
-
-    def emit(row):
-        rows.append(row)
-        print(f"[bench] {row}", file=sys.stderr, flush=True)
-
-    if want(0):
-        emit(dict(config=0, **gemv_case(torch, ops, synth, dev, 4, 1, 8192, 2048, 64,
-                                        torch.bfloat16, timer, st, wu)))
-    if want(1):
-        for (K, N) in [(2048, 2048), (2048, 512), (2048, 8192), (8192, 2048)]:
-            for M in (2, 4, 8, 16, 32):
-                emit(dict(config=1, **gemv_case(torch, ops, synth, dev, 4, M, N, K, 64,
-                                                torch.bfloat16, timer, st, wu)))
-    if want(2):
-        for M in (1, 8, 32):
-            emit(dict(config=2, **gemv_case(torch, ops, synth, dev, 8, M, 131072, 2048, 64,
-                                            torch.bfloat16, timer, 20, 3)))
-    if want(4):
-        for M in (1024, 32):
-            for stacked in (False, True):
-                emit(chain_case(torch, ops, synth, dev, M, timer, stacked=stacked))
-    for fused in (False, True):
-        if not want(4 if fused else 3):
-            continue
-        for M in (256, 1024, 1472):
-            for (K, N) in [(2048, 8192), (8192, 2048), (2048, 2560)]:
-                emit(dict(config=4 if fused else 3,
-                          **gemm_case(torch, ops, synth, oracle, dev, M, N, K, fused,
-                                      timer, 30, 3)))
-    if only is None:
-        for (K, N) in [(2048, 2048), (2048, 8192), (7680, 2048), (8192, 2048)]:
-            emit(dict(row="fused-decode", **fused_decode_case(torch, ops, synth, dev, N, K,
-                                                             timer, st, wu)))
-        for (M, N, K) in [(1, 16, 2048), (32, 16, 2048), (8, 131072, 2048), (32, 131072, 2048)]:
-            emit(dict(row="gemm_naive", **naive_case(torch, ops, dev, M, N, K, timer, 20, 3)))
-    return rows
 
 
 if __name__ == "__main__":

@@ -18,7 +18,18 @@
  *    enqueued when a check fails. The reference kernels have no error path
  *    (unsupported shapes are silently skipped, shaders/batch.metal:156);
  *    here they are rejected.
- *  - Thread-safe across distinct streams; calls on one stream are ordered.
+ *  - Calls on one stream are ordered. The split-K GEMMs and the batched
+ *    GEMV at M > 8 with K >= 8192 keep fp32 partials in one workspace per
+ *    device: such calls that overlap on different streams of one device
+ *    race, so a caller that uses several streams per device must order them
+ *    (events) or serialise the calls. Every other entry point only touches
+ *    its arguments and may overlap freely. The workspace grows (hipMalloc) on
+ *    the first split-K call that needs more than it holds, which is refused
+ *    while the stream is being captured into a graph (MIORI_E_HIP): run each
+ *    shape once eagerly before capturing it. Superseded workspaces are never
+ *    freed, so a captured graph stays valid for the life of the process.
+ *    The reference drives one encoder per engine from one host thread
+ *    (src/engine.h:176-177).
  *
  * Weight format (MLX affine, src/cpu_ref.h:25-45): W[N][K] quantized in
  * groups of `group` consecutive elements along K.
@@ -38,7 +49,7 @@
 extern "C" {
 #endif
 
-#define MIORI_HIP_ABI_VERSION 1
+#define MIORI_HIP_ABI_VERSION 2
 
 /* status codes */
 #define MIORI_OK 0
@@ -47,6 +58,7 @@ extern "C" {
 #define MIORI_E_ALIGN (-3)     /* pointer misaligned for the kernel's loads */
 #define MIORI_E_DTYPE (-4)     /* unknown out_dtype */
 #define MIORI_E_HIP (-5)       /* a HIP runtime call failed */
+#define MIORI_E_SCRATCH (-6)   /* split-K partials exceed a fixed scratch buffer */
 
 /* output element types */
 #define MIORI_F32 0
@@ -137,6 +149,23 @@ int miori_gemm_bf16(const void* A, const void* B, void* C, uint32_t M,
 int miori_gemm_q4(const void* A, const void* q, const void* scales,
                   const void* biases, void* C, uint32_t M, uint32_t N, uint32_t K,
                   uint32_t group, int out_dtype, miori_stream stream);
+
+/* Batch-engine projection policy: C[M][N] = A[M][K] . W^T for 4-bit MLX
+ * weights W (q, scales, biases) with an optional bf16 cache of the same W
+ * (row-major [N][K], as miori_dequant_q4_tile writes it; NULL if none).
+ * Replaces BatchEngine::linear (src/batch.cpp:223-230), which runs the exact
+ * 4-bit gemv4_b at <= 4 active slots and otherwise the bf16-cache GEMM
+ * (gemm_mpp32 up to 32 rows, gemm_mpp beyond). Here:
+ *  - M <= 32: the exact batched 4-bit GEMV (miori_gemv_q4_batched). It reads
+ *    a quarter of the bytes of the bf16 cache and is the faster of the two at
+ *    every M = 1..32 on the decode projection shapes, so the cache is never
+ *    read for decode;
+ *  - M > 32: miori_gemm_bf16 on the cache when one is given, else the fused
+ *    4-bit GEMM (miori_gemm_q4).
+ * Shape rules are those of the entry point taken. */
+int miori_linear_q4(const void* A, const void* q, const void* scales, const void* biases,
+                    const void* bf16_cache, void* C, uint32_t M, uint32_t N, uint32_t K,
+                    uint32_t group, int out_dtype, miori_stream stream);
 
 /* Strided GEMM for any shape: C[m*ldc + n] = sum_k A[m*lda + k] * B[n*ldb + k],
  * bf16 operands, fp32 output, each output one fp32 FMA chain over k = 0..K-1

@@ -14,6 +14,8 @@ using namespace miori;
 namespace {
 
 constexpr uint64_t kMaxBytes = 0xFFFFFFF0ull;
+// miori_linear_q4 takes the exact 4-bit batched GEMV up to this many rows.
+constexpr uint32_t kLinearExactMaxM = 32;
 
 inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
 
@@ -79,6 +81,7 @@ const char* miori_status_string(int status) {
         case MIORI_E_ALIGN: return "misaligned pointer";
         case MIORI_E_DTYPE: return "unknown output dtype";
         case MIORI_E_HIP: return "HIP runtime error";
+        case MIORI_E_SCRATCH: return "split-K partials exceed the fixed scratch buffer";
     }
     return "unknown status";
 }
@@ -162,22 +165,47 @@ int miori_gemm_bf16(const void* A, const void* B, void* C, uint32_t M, uint32_t 
                                   out_dtype == MIORI_BF16, (hipStream_t)stream));
 }
 
-int miori_gemm_q4(const void* A, const void* q, const void* scales, const void* biases,
-                  void* C, uint32_t M, uint32_t N, uint32_t K, uint32_t group,
-                  int out_dtype, miori_stream stream) {
+}  // extern "C"
+
+// miori_gemm_q4 with the stream already cast; under a ScratchScope a split
+// whose partials do not fit the fixed buffer returns MIORI_E_SCRATCH.
+int miori::gemm_q4_entry(const void* A, const void* q, const void* scales, const void* biases,
+                         void* C, uint32_t M, uint32_t N, uint32_t K, uint32_t group,
+                         int out_dtype, hipStream_t stream) {
     int st = check_gemm(A, C, M, N, K, out_dtype);
     if (st) return st;
     if (!q || !scales || !biases) return MIORI_E_NULL;
     if (!(group == 32 || group == 64 || group == 128) || K % group != 0) return MIORI_E_SHAPE;
     if (!aligned(q, 16) || !aligned(scales, 2) || !aligned(biases, 2)) return MIORI_E_ALIGN;
+    hipError_t e;
     // Small M runs on the skinny kernel, with the bf16 GEMM's routing (so the
     // fused product stays bit-identical to dequant + bf16 GEMM; that needs
     // K / group to be a multiple of 8 and 16-byte aligned scales / biases).
     if (M <= 32 && skinny_ok(2, M, N, K, group, scales, biases) && skinny_supported(3, M, N, K, 64))
-        return hip_status(launch_skinny(2, A, q, scales, biases, C, M, N, K, group,
-                                        out_dtype == MIORI_BF16, (hipStream_t)stream));
-    return hip_status(launch_gemm(A, nullptr, q, scales, biases, C, M, N, K, group,
-                                  out_dtype == MIORI_BF16, (hipStream_t)stream));
+        e = launch_skinny(2, A, q, scales, biases, C, M, N, K, group, out_dtype == MIORI_BF16,
+                          stream);
+    else
+        e = launch_gemm(A, nullptr, q, scales, biases, C, M, N, K, group,
+                        out_dtype == MIORI_BF16, stream);
+    if (e == hipErrorOutOfMemory && ScratchScope::current()) return MIORI_E_SCRATCH;
+    return hip_status(e);
+}
+
+extern "C" {
+
+int miori_gemm_q4(const void* A, const void* q, const void* scales, const void* biases,
+                  void* C, uint32_t M, uint32_t N, uint32_t K, uint32_t group,
+                  int out_dtype, miori_stream stream) {
+    return gemm_q4_entry(A, q, scales, biases, C, M, N, K, group, out_dtype, (hipStream_t)stream);
+}
+
+int miori_linear_q4(const void* A, const void* q, const void* scales, const void* biases,
+                    const void* bf16_cache, void* C, uint32_t M, uint32_t N, uint32_t K,
+                    uint32_t group, int out_dtype, miori_stream stream) {
+    if (M <= kLinearExactMaxM)
+        return miori_gemv_q4_batched(q, scales, biases, A, C, M, N, K, group, out_dtype, stream);
+    if (bf16_cache) return miori_gemm_bf16(A, bf16_cache, C, M, N, K, out_dtype, stream);
+    return miori_gemm_q4(A, q, scales, biases, C, M, N, K, group, out_dtype, stream);
 }
 
 int miori_gemm_naive(const void* A, const void* B, float* C, uint32_t M, uint32_t N,

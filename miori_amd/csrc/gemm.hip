@@ -548,7 +548,7 @@ hipError_t launch_cfg(const void* A, const void* B, const void* q, const void* s
     static const int remap = tuning_env("MIORI_GEMM_REMAP", 1);
     float* part = nullptr;
     if (SK > 1) {
-        const hipError_t e = workspace_get(st, (size_t)SK * M * N * 4, &part);
+        const hipError_t e = scratch_get(st, (size_t)SK * M * N * 4, &part);
         if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL((gemm_kernel<BM, BN, Q4, G>), dim3(ntiles * SK), dim3(256), 0, st,

@@ -43,8 +43,39 @@ hipError_t launch_skinny(int mode, const void* X, const void* W, const void* S, 
                          void* Y, uint32_t M, uint32_t N, uint32_t K, uint32_t G, int out_bf16,
                          hipStream_t st);
 
-// Split-K partials workspace of the current device (grown outside graph capture).
+// Split-K partials workspace of the current device: grown outside graph
+// capture only (st is the stream checked for capture), superseded buffers
+// kept until the process ends.
 hipError_t workspace_get(hipStream_t st, size_t bytes, float** part);
+
+// A caller-provided fixed scratch buffer (device memory the library does not
+// allocate). While a ScratchScope is alive on a host thread, every split-K
+// launch that thread makes takes its partials from that buffer instead of
+// the per-stream workspace, and fails with hipErrorOutOfMemory, before
+// anything is enqueued, when the partials do not fit.
+struct Scratch {
+    float* ptr;
+    size_t bytes;
+};
+class ScratchScope {
+public:
+    explicit ScratchScope(const Scratch* s) : prev_(current_) { current_ = s; }
+    ~ScratchScope() { current_ = prev_; }
+    ScratchScope(const ScratchScope&) = delete;
+    ScratchScope& operator=(const ScratchScope&) = delete;
+    static const Scratch* current() { return current_; }
+
+private:
+    const Scratch* prev_;
+    static thread_local const Scratch* current_;
+};
+// Checked fused 4-bit GEMM behind miori_gemm_q4 (returns a MIORI_* status).
+int gemm_q4_entry(const void* A, const void* q, const void* scales, const void* biases, void* C,
+                  uint32_t M, uint32_t N, uint32_t K, uint32_t group, int out_dtype,
+                  hipStream_t stream);
+// Partials buffer for a split-K launch: the scoped fixed scratch if one is
+// active on this thread, else workspace_get.
+hipError_t scratch_get(hipStream_t st, size_t bytes, float** part);
 // C[i] = sum over k = 0..SK-1 of part[k * MN + i], in that order, as fp32 or
 // bf16 (MN a multiple of 8).
 hipError_t launch_splitk_reduce(const float* part, void* C, size_t MN, uint32_t SK, int out_bf16,

@@ -520,7 +520,7 @@ hipError_t launch_sk(const void* X, const void* W, const void* S, const void* B,
     const uint32_t nwg = (N + 16 * NT - 1) / (16 * NT);
     float* part = nullptr;
     if (SK > 1) {
-        const hipError_t e = workspace_get(st, (size_t)SK * M * N * 4, &part);
+        const hipError_t e = scratch_get(st, (size_t)SK * M * N * 4, &part);
         if (e != hipSuccess) return e;
     }
     using C = Sk<MODE, MT, NT, G, NBW, NWV>;

@@ -1,15 +1,24 @@
-// Device workspace for split-K partial sums: one per device, grown on demand
-// and kept until the process ends. Growing allocates (hipMalloc), so it is
-// refused while the stream is being captured into a graph; a first call of
-// the same or larger size outside capture sizes it. Every split-K launch on
-// a device uses this one workspace: launches on one stream are ordered,
-// launches that overlap on different streams of one device race.
+// Device workspace for split-K partial sums, one per device.
+//
+// Lifetime: a workspace is never freed. When a larger request arrives, a new
+// buffer is allocated and the old one is retained until the process ends,
+// because a HIP graph captured earlier may still hold the old address and
+// replay into it later. Growing allocates (hipMalloc), so it is refused while
+// the stream is being captured into a graph; a first call of the same or
+// larger size outside capture sizes the buffer.
+//
+// Concurrency: every split-K launch on a device uses this one buffer.
+// Launches on one stream are ordered; split-K products that overlap on
+// different streams of one device race on the partials. (One buffer per
+// device, rather than per stream, is what lets a product be captured on a
+// graph-capture stream after an eager call on another stream sized it.)
 #include "kernels.hpp"
 
 #include <hip/hip_runtime.h>
 
 #include <map>
 #include <mutex>
+#include <vector>
 
 namespace miori {
 
@@ -22,6 +31,7 @@ struct Workspace {
 
 std::mutex g_mu;
 std::map<int, Workspace> g_ws;
+std::vector<float*> g_retired;  // superseded buffers, kept for captured graphs
 
 }  // namespace
 
@@ -36,17 +46,28 @@ hipError_t workspace_get(hipStream_t st, size_t bytes, float** part) {
         e = hipStreamIsCapturing(st, &cs);
         if (e != hipSuccess) return e;
         if (cs != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
-        e = hipStreamSynchronize(st);  // earlier launches may still read the old buffer
+        // Earlier launches on other streams may still read the old buffer;
+        // it is retired, not freed, so they (and captured graphs) stay valid.
+        float* p = nullptr;
+        e = hipMalloc((void**)&p, bytes);
         if (e != hipSuccess) return e;
-        if (w.part) (void)hipFree(w.part);
-        w.part = nullptr;
-        w.bytes = 0;
-        e = hipMalloc((void**)&w.part, bytes);
-        if (e != hipSuccess) return e;
+        if (w.part) g_retired.push_back(w.part);
+        w.part = p;
         w.bytes = bytes;
     }
     *part = w.part;
     return hipSuccess;
+}
+
+thread_local const Scratch* ScratchScope::current_ = nullptr;
+
+hipError_t scratch_get(hipStream_t st, size_t bytes, float** part) {
+    if (const Scratch* fixed = ScratchScope::current()) {
+        if (bytes > fixed->bytes) return hipErrorOutOfMemory;
+        *part = fixed->ptr;
+        return hipSuccess;
+    }
+    return workspace_get(st, bytes, part);
 }
 
 }  // namespace miori

@@ -87,6 +87,11 @@ private:
 struct Metal {
     int device = 0;
     hipStream_t stream = nullptr;
+    // Quantisation group size of the raw-buffer ops (gemv4_raw, gemv8_off),
+    // which carry no scale-tensor shape to read it from. Default: the
+    // reference's kGroup (config/m6.h:48). One value per device context, so
+    // engines with different weight formats keep separate Metal objects.
+    uint32_t raw_group = 32;
 
     bool init(const std::string& unused_library_path, std::string& err);
     MTL::Buffer* new_buffer(size_t bytes, bool shared = true);

@@ -12,8 +12,6 @@ namespace miori {
 
 namespace {
 
-uint32_t g_raw_group = 32;
-
 void check(int st, const char* fn) {
     if (st != MIORI_OK)
         throw std::runtime_error(std::string(fn) + ": " + miori_status_string(st));
@@ -103,9 +101,6 @@ void dequant_t(int bits, bool tile, MTL::ComputeCommandEncoder* e, const Weights
 
 }  // namespace
 
-void set_raw_group(uint32_t group) { g_raw_group = group; }
-uint32_t raw_group() { return g_raw_group; }
-
 void gemv4(Metal&, MTL::ComputeCommandEncoder* e, const Weights& w, const Tensor& q,
            const Tensor& s, const Tensor& b, MTL::Buffer* x, MTL::Buffer* y, uint32_t N,
            uint32_t K) {
@@ -158,9 +153,14 @@ void gemv4x2(Metal& m, MTL::ComputeCommandEncoder* e, const Weights& w, const Te
     gemv4(m, e, w, q, s, b, x, y, N, K);
 }
 
-void gemv4_raw(Metal&, MTL::ComputeCommandEncoder* e, MTL::Buffer* q, MTL::Buffer* s,
+void gemv4_raw(Metal& m, MTL::ComputeCommandEncoder* e, MTL::Buffer* q, MTL::Buffer* s,
                MTL::Buffer* b, MTL::Buffer* x, MTL::Buffer* y, uint32_t N, uint32_t K) {
-    const uint32_t G = g_raw_group;
+    gemv4_raw(m, e, q, s, b, x, y, N, K, m.raw_group);
+}
+
+void gemv4_raw(Metal&, MTL::ComputeCommandEncoder* e, MTL::Buffer* q, MTL::Buffer* s,
+               MTL::Buffer* b, MTL::Buffer* x, MTL::Buffer* y, uint32_t N, uint32_t K,
+               uint32_t G) {
     if (G == 0 || K % G) throw std::runtime_error("gemv4_raw: K is not a multiple of the group");
     need(q, 0, (uint64_t)N * K / 2, "q");
     need(s, 0, (uint64_t)N * (K / G) * 2, "s");
@@ -174,10 +174,15 @@ void gemv4_raw(Metal&, MTL::ComputeCommandEncoder* e, MTL::Buffer* q, MTL::Buffe
           "gemv4_raw");
 }
 
-void gemv8_off(Metal&, MTL::ComputeCommandEncoder* e, MTL::Buffer* wbuf, uint32_t qoff,
+void gemv8_off(Metal& m, MTL::ComputeCommandEncoder* e, MTL::Buffer* wbuf, uint32_t qoff,
                uint32_t soff, uint32_t boff, MTL::Buffer* x, MTL::Buffer* y, uint32_t N,
                uint32_t K, uint32_t xoff, uint32_t yoff) {
-    const uint32_t G = g_raw_group;
+    gemv8_off(m, e, wbuf, qoff, soff, boff, x, y, N, K, xoff, yoff, m.raw_group);
+}
+
+void gemv8_off(Metal&, MTL::ComputeCommandEncoder* e, MTL::Buffer* wbuf, uint32_t qoff,
+               uint32_t soff, uint32_t boff, MTL::Buffer* x, MTL::Buffer* y, uint32_t N,
+               uint32_t K, uint32_t xoff, uint32_t yoff, uint32_t G) {
     if (G == 0 || K % G) throw std::runtime_error("gemv8_off: K is not a multiple of the group");
     need(wbuf, qoff, (uint64_t)N * K, "q");
     need(wbuf, soff, (uint64_t)N * (K / G) * 2, "s");
@@ -261,6 +266,25 @@ void gemm_mpp(Metal& m, MTL::ComputeCommandEncoder* e, MTL::Buffer* A, MTL::Buff
 void gemm_mpp32(Metal& m, MTL::ComputeCommandEncoder* e, MTL::Buffer* A, MTL::Buffer* B,
                 MTL::Buffer* C, uint32_t M, uint32_t N, uint32_t K, uint32_t boff) {
     gemm_mpp_off(m, e, A, B, C, M, N, K, 0, boff, 0);
+}
+
+void linear(Metal&, MTL::ComputeCommandEncoder* e, const Weights& w, const Tensor& q,
+            const Tensor& s, const Tensor& b, MTL::Buffer* A, MTL::Buffer* C, uint32_t N,
+            uint32_t K, uint32_t B, MTL::Buffer* bf16_cache, uint32_t cache_off) {
+    QArgs a = qargs(e, w, q, s, b, N, K, 4);
+    need(A, 0, (uint64_t)B * K * 2, "A");
+    need(C, 0, (uint64_t)B * N * 4, "C");
+    const void* cache = nullptr;
+    if (bf16_cache) {
+        need(bf16_cache, cache_off, (uint64_t)N * K * 2, "bf16 cache");
+        e->use_in(bf16_cache);
+        cache = at(bf16_cache, cache_off);
+    }
+    e->use_in(A);
+    e->use_out(C);
+    check(miori_linear_q4(A->gpu(), a.q, a.s, a.b, cache, C->gpu(), B, N, K, a.G, MIORI_F32,
+                          e->stream()),
+          "linear");
 }
 
 void gemm_q4(Metal&, MTL::ComputeCommandEncoder* e, MTL::Buffer* A, const Weights& w,

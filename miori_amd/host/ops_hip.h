@@ -8,8 +8,8 @@
 // a failed call throws std::runtime_error. Differences, all widenings:
 //  * the quantisation group size is read from the scale tensor's shape
 //    (group = K / scales.cols()); the raw-buffer entries, which carry no
-//    shapes, use raw_group() (32 by default, the reference's kGroup,
-//    config/m6.h:48);
+//    shapes, take it from Metal::raw_group (32 by default, the reference's
+//    kGroup, config/m6.h:48) or from an explicit `group` argument;
 //  * gemv4_b / gemv8_b / gemv8_b_off take any 1 <= B <= 32 and write B rows
 //    (the reference returns early for B > 4 and always writes 4 rows,
 //    shaders/batch.metal:156, :203);
@@ -23,9 +23,6 @@
 #include <cstdint>
 
 namespace miori {
-
-void set_raw_group(uint32_t group);
-uint32_t raw_group();
 
 // src/ops.h:8-10
 void gemv4(Metal& m, MTL::ComputeCommandEncoder* e, const Weights& w,
@@ -74,6 +71,10 @@ void gemv4x4(Metal& m, MTL::ComputeCommandEncoder* e, const Weights& w,
 void gemv4_raw(Metal& m, MTL::ComputeCommandEncoder* e, MTL::Buffer* q,
                MTL::Buffer* s, MTL::Buffer* b, MTL::Buffer* x, MTL::Buffer* y,
                uint32_t N, uint32_t K);
+// gemv4_raw with an explicit group size (no reference counterpart).
+void gemv4_raw(Metal& m, MTL::ComputeCommandEncoder* e, MTL::Buffer* q,
+               MTL::Buffer* s, MTL::Buffer* b, MTL::Buffer* x, MTL::Buffer* y,
+               uint32_t N, uint32_t K, uint32_t group);
 // src/ops.h:126-128
 void gemv4x2(Metal& m, MTL::ComputeCommandEncoder* e, const Weights& w,
              const Tensor& q, const Tensor& s, const Tensor& b,
@@ -83,6 +84,11 @@ void gemv8_off(Metal& m, MTL::ComputeCommandEncoder* e, MTL::Buffer* wbuf,
                uint32_t qoff, uint32_t soff, uint32_t boff, MTL::Buffer* x,
                MTL::Buffer* y, uint32_t N, uint32_t K, uint32_t xoff,
                uint32_t yoff);
+// gemv8_off with an explicit group size (no reference counterpart).
+void gemv8_off(Metal& m, MTL::ComputeCommandEncoder* e, MTL::Buffer* wbuf,
+               uint32_t qoff, uint32_t soff, uint32_t boff, MTL::Buffer* x,
+               MTL::Buffer* y, uint32_t N, uint32_t K, uint32_t xoff,
+               uint32_t yoff, uint32_t group);
 // src/ops.h:164-166
 void gemv4_b(Metal& m, MTL::ComputeCommandEncoder* e, const Weights& w,
              const Tensor& q, const Tensor& s, const Tensor& b, MTL::Buffer* x,
@@ -104,6 +110,14 @@ void dequant8(Metal& m, MTL::ComputeCommandEncoder* e, const Weights& w,
 void gemm_mpp32(Metal& m, MTL::ComputeCommandEncoder* e, MTL::Buffer* A,
                 MTL::Buffer* B, MTL::Buffer* C, uint32_t M, uint32_t N, uint32_t K,
                 uint32_t boff = 0);
+
+// BatchEngine::linear (src/batch.cpp:223-230) as a free function: C[B][N] =
+// A[B][K] . W^T, the exact 4-bit batched GEMV for B <= 32, else the bf16
+// cache GEMM when `bf16_cache` is given (the cache tensor starts at byte
+// `cache_off`, row-major [N][K]), else the fused 4-bit GEMM.
+void linear(Metal& m, MTL::ComputeCommandEncoder* e, const Weights& w, const Tensor& q,
+            const Tensor& s, const Tensor& b, MTL::Buffer* A, MTL::Buffer* C, uint32_t N,
+            uint32_t K, uint32_t B, MTL::Buffer* bf16_cache = nullptr, uint32_t cache_off = 0);
 
 // No reference counterpart: the fused 4-bit GEMM (dequantisation inside the
 // GEMM's LDS staging), replacing the reference's dequant_tile + gemm_mpp

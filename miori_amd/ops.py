@@ -166,6 +166,22 @@ def gemm_q4(A, q, s, b, C, M, N, K, group=64, stream=None):
               _stream(stream))
 
 
+def linear(A, q, s, b, C, M, N, K, group=64, bf16_cache=None, stream=None):
+    """Batch-engine projection C[M][N] = A[M][K] . W^T with the dispatch
+    policy of BatchEngine::linear (src/batch.cpp:223-230): the exact 4-bit
+    batched GEMV for M <= 32, else the bf16-cache GEMM when a cache
+    (row-major [N][K] bf16, from dequant_tile) is given, else the fused 4-bit
+    GEMM."""
+    if K % group:
+        raise MioriError("miori_linear_q4", -2, "K must be a multiple of the group size")
+    qp, sp, bp = _qargs(q, s, b, N, K, group, 4)
+    ap = _ptr(A, "A", M * K * 2)
+    cp = _ptr(C, "C", M * N * C.element_size())
+    cache = 0 if bf16_cache is None else _ptr(bf16_cache, "bf16_cache", N * K * 2)
+    _lib.call("miori_linear_q4", ap, qp, sp, bp, cache or None, cp, M, N, K, group,
+              _out_dtype(C), _stream(stream))
+
+
 def gemm_naive(A, B, C, M, N, K, lda, ldb, ldc, aoff=0, boff=0, coff=0, stream=None):
     """C[m*ldc + n] = sum_k A[m*lda + k] * B[n*ldb + k] for any shape, bf16
     operands, fp32 C, one sequential fp32 FMA chain per output (src/ops.h:30-32;

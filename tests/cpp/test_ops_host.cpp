@@ -297,6 +297,165 @@ int main(int argc, char** argv) {
         C->release(); delete C;
     }
 
+    // ---- raw-buffer and offset entries the engines use: gemv8_off (batched
+    // lm_head, src/batch.cpp:596-600) at group 64 through the Metal's
+    // raw_group and through the explicit-group overload, gemv4_raw on its own
+    // buffers, gemv8_b on 8 rows, dequant4 / dequant8 bit-exact
+    {
+        const Tensor& eq = w.get("embed_tokens.weight");
+        const Tensor& esc = w.get("embed_tokens.scales");
+        const Tensor& ebi = w.get("embed_tokens.biases");
+        MTL::Buffer* logits = m.new_buffer((size_t)8 * NV * 4);
+        std::vector<double> r8((size_t)8 * NV);
+        xp = (uint16_t*)x->contents();
+        // rows 2 and 5 of x, written at output rows 1 and 6
+        m.raw_group = (uint32_t)G;
+        auto cb = m.begin();
+        auto e = cb->computeCommandEncoder();
+        gemv8_off(m, e, w.buffer(), (uint32_t)eq.begin, (uint32_t)esc.begin, (uint32_t)ebi.begin, x,
+                  logits, (uint32_t)NV, (uint32_t)K, (uint32_t)(2 * K * 2), (uint32_t)(1 * NV * 4));
+        m.raw_group = 32;
+        gemv8_off(m, e, w.buffer(), (uint32_t)eq.begin, (uint32_t)esc.begin, (uint32_t)ebi.begin, x,
+                  logits, (uint32_t)NV, (uint32_t)K, (uint32_t)(5 * K * 2), (uint32_t)(6 * NV * 4),
+                  (uint32_t)G);
+        m.submit(cb, true);
+        const float* lg = (const float*)logits->contents();
+        xp = (uint16_t*)x->contents();
+        orc_gemv8_f64((const uint32_t*)eq.ptr, (const uint16_t*)esc.ptr, (const uint16_t*)ebi.ptr,
+                      xp + 2 * K, r8.data(), 1, NV, K, G, 8);
+        expect(close_enough(lg + NV, r8.data(), NV, "gemv8_off raw_group=64"),
+               "gemv8_off (Metal::raw_group = 64) vs oracle");
+        orc_gemv8_f64((const uint32_t*)eq.ptr, (const uint16_t*)esc.ptr, (const uint16_t*)ebi.ptr,
+                      xp + 5 * K, r8.data(), 1, NV, K, G, 8);
+        expect(close_enough(lg + 6 * NV, r8.data(), NV, "gemv8_off group=64"),
+               "gemv8_off (explicit group 64) vs oracle");
+
+        cb = m.begin();
+        e = cb->computeCommandEncoder();
+        gemv8_b(m, e, w, eq, esc, ebi, x, logits, (uint32_t)NV, (uint32_t)K, 8);
+        m.submit(cb, true);
+        xp = (uint16_t*)x->contents();
+        orc_gemv8_f64((const uint32_t*)eq.ptr, (const uint16_t*)esc.ptr, (const uint16_t*)ebi.ptr,
+                      xp, r8.data(), 8, NV, K, G, 8);
+        expect(close_enough((const float*)logits->contents(), r8.data(), 8 * (size_t)NV, "gemv8_b"),
+               "gemv8_b B=8 vs oracle");
+
+        // gemv4_raw: q / scales / biases in buffers of their own
+        MTL::Buffer* rq = m.new_buffer(q.bytes(), false);
+        MTL::Buffer* rs = m.new_buffer(s.bytes(), false);
+        MTL::Buffer* rb = m.new_buffer(b.bytes(), false);
+        rq->upload(q.ptr, q.bytes());
+        rs->upload(s.ptr, s.bytes());
+        rb->upload(b.ptr, b.bytes());
+        cb = m.begin();
+        e = cb->computeCommandEncoder();
+        gemv4_raw(m, e, rq, rs, rb, x, y, (uint32_t)N, (uint32_t)K, (uint32_t)G);
+        m.submit(cb, true);
+        xp = (uint16_t*)x->contents();
+        orc_gemv4_f64((const uint32_t*)q.ptr, (const uint16_t*)s.ptr, (const uint16_t*)b.ptr, xp,
+                      ref.data(), 1, N, K, G, 8);
+        expect(close_enough((const float*)y->contents(), ref.data(), N, "gemv4_raw"),
+               "gemv4_raw (group 64) vs oracle");
+        rq->release(); delete rq;
+        rs->release(); delete rs;
+        rb->release(); delete rb;
+
+        MTL::Buffer* d4 = m.new_buffer((size_t)N * K * 2, false);
+        MTL::Buffer* d8 = m.new_buffer((size_t)NV * K * 2, false);
+        cb = m.begin();
+        e = cb->computeCommandEncoder();
+        dequant4(m, e, w, q, s, b, d4, (uint32_t)N, (uint32_t)K);
+        dequant8(m, e, w, eq, esc, ebi, d8, (uint32_t)NV, (uint32_t)K);
+        m.submit(cb, true);
+        std::vector<uint16_t> got4((size_t)N * K), ref4((size_t)N * K);
+        std::vector<uint16_t> got8((size_t)NV * K), ref8((size_t)NV * K);
+        d4->download(got4.data(), got4.size() * 2);
+        d8->download(got8.data(), got8.size() * 2);
+        orc_dequant4_bf16((const uint32_t*)q.ptr, (const uint16_t*)s.ptr, (const uint16_t*)b.ptr,
+                          ref4.data(), N, K, G);
+        orc_dequant8_bf16((const uint32_t*)eq.ptr, (const uint16_t*)esc.ptr,
+                          (const uint16_t*)ebi.ptr, ref8.data(), NV, K, G);
+        expect(got4 == ref4, "dequant4 bit-exact vs oracle");
+        expect(got8 == ref8, "dequant8 bit-exact vs oracle");
+        d4->release(); delete d4;
+        d8->release(); delete d8;
+        logits->release(); delete logits;
+    }
+
+    // ---- gemm_mpp_off with non-zero A / B / C offsets (src/engine.cpp:508-518),
+    // gemm_mpp32 on 32 rows, and the batch-engine linear policy
+    // (src/batch.cpp:223-230) at 8 rows (exact GEMV) and 96 rows (cache GEMM,
+    // and the fused GEMM without a cache)
+    {
+        const uint32_t M = 96, aoff = 3 * K * 2, boff = 4096, coff = 5 * N * 4;
+        MTL::Buffer* cache = m.new_buffer(boff + (size_t)N * K * 2, false);
+        MTL::Buffer* A = m.new_buffer(aoff + (size_t)M * K * 2);
+        MTL::Buffer* C = m.new_buffer(coff + (size_t)M * N * 4);
+        MTL::Buffer* C2 = m.new_buffer((size_t)M * N * 4);
+        uint16_t* ap = (uint16_t*)A->contents();
+        for (size_t i = 0; i < aoff / 2 + (size_t)M * K; ++i)
+            ap[i] = orc_f32_to_bf16(cosf(0.07f * (float)i));
+        auto cb = m.begin();
+        auto e = cb->computeCommandEncoder();
+        dequant_tile(m, e, w, q, s, b, cache, (uint32_t)N, (uint32_t)K, boff);
+        gemm_mpp_off(m, e, A, cache, C, M, (uint32_t)N, (uint32_t)K, aoff, boff, coff);
+        m.submit(cb, true);
+        std::vector<uint16_t> cref16((size_t)N * K);
+        orc_dequant4_bf16((const uint32_t*)q.ptr, (const uint16_t*)s.ptr, (const uint16_t*)b.ptr,
+                          cref16.data(), N, K, G);
+        std::vector<int64_t> rows;
+        for (uint32_t r = 0; r < M; ++r) rows.push_back(r);
+        std::vector<double> cref((size_t)M * N);
+        ap = (uint16_t*)A->contents();
+        orc_gemm_bf16_f64(ap + aoff / 2, cref16.data(), cref.data(), M, N, K, rows.data(), M, 8);
+        const float* cp = (const float*)((const char*)C->contents() + coff);
+        expect(close_enough(cp, cref.data(), (size_t)M * N, "gemm_mpp_off"),
+               "gemm_mpp_off (aoff, boff, coff != 0) vs oracle");
+
+        // gemm_mpp32: rows 0..31 of the same product
+        cb = m.begin();
+        e = cb->computeCommandEncoder();
+        gemm_mpp32(m, e, A, cache, C2, 32, (uint32_t)N, (uint32_t)K, boff);
+        m.submit(cb, true);
+        ap = (uint16_t*)A->contents();
+        orc_gemm_bf16_f64(ap, cref16.data(), cref.data(), 32, N, K, rows.data(), 32, 8);
+        expect(close_enough((const float*)C2->contents(), cref.data(), (size_t)32 * N, "gemm_mpp32"),
+               "gemm_mpp32 vs oracle");
+
+        // linear: 8 rows take the exact 4-bit GEMV (fp64-of-fp32-dequant oracle)
+        cb = m.begin();
+        e = cb->computeCommandEncoder();
+        linear(m, e, w, q, s, b, x, C2, (uint32_t)N, (uint32_t)K, 8, cache, boff);
+        m.submit(cb, true);
+        xp = (uint16_t*)x->contents();
+        std::vector<double> rl((size_t)8 * N);
+        orc_gemv4_f64((const uint32_t*)q.ptr, (const uint16_t*)s.ptr, (const uint16_t*)b.ptr, xp,
+                      rl.data(), 8, N, K, G, 8);
+        expect(close_enough((const float*)C2->contents(), rl.data(), (size_t)8 * N, "linear B=8"),
+               "linear B=8 (exact 4-bit) vs oracle");
+        // 96 rows with the cache: the bf16 GEMM; without: the fused GEMM, same values
+        cb = m.begin();
+        e = cb->computeCommandEncoder();
+        linear(m, e, w, q, s, b, A, C2, (uint32_t)N, (uint32_t)K, M, cache, boff);
+        m.submit(cb, true);
+        ap = (uint16_t*)A->contents();
+        orc_gemm_bf16_f64(ap, cref16.data(), cref.data(), M, N, K, rows.data(), M, 8);
+        std::vector<float> lc((size_t)M * N);
+        memcpy(lc.data(), C2->contents(), lc.size() * 4);
+        expect(close_enough(lc.data(), cref.data(), (size_t)M * N, "linear B=96 cache"),
+               "linear B=96 (bf16 cache GEMM) vs oracle");
+        cb = m.begin();
+        e = cb->computeCommandEncoder();
+        linear(m, e, w, q, s, b, A, C2, (uint32_t)N, (uint32_t)K, M);
+        m.submit(cb, true);
+        expect(memcmp(lc.data(), C2->contents(), lc.size() * 4) == 0,
+               "linear B=96 without cache (fused GEMM) bit-identical to the cache GEMM");
+        cache->release(); delete cache;
+        A->release(); delete A;
+        C->release(); delete C;
+        C2->release(); delete C2;
+    }
+
     // ---- errors surface as exceptions, as the reference's Metal::pso does
     {
         bool threw = false;

@@ -30,8 +30,8 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_status_strings():
     lib = _lib.load()
-    assert lib.miori_abi_version() == 1
-    for st in (0, -1, -2, -3, -4, -5):
+    assert lib.miori_abi_version() == 2
+    for st in (0, -1, -2, -3, -4, -5, -6):
         assert lib.miori_status_string(st)
     assert lib.miori_status_string(-99) == b"unknown status"
 

@@ -113,3 +113,47 @@ def test_graph_replay_matches_eager(dev, name):
         g.replay()
         torch.cuda.synchronize()
         np.testing.assert_array_equal(ops.bits_of(out), ref, err_msg=f"{name} replay {r}")
+
+
+def test_graph_replay_after_workspace_growth(dev):
+    """A graph captured with a split-K product keeps the workspace address
+    it was captured with. An eager split-K product that needs a larger
+    workspace allocates a new one and must leave the old one alive: every
+    replay after the growth reproduces the eager result bit for bit."""
+    say("graph replay after split-K workspace growth")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+
+    def quant(N, K):
+        q = torch.randint(-2 ** 31, 2 ** 31 - 1, (N, K // 8), dtype=torch.int32, device=dev,
+                          generator=gen)
+        s = (0.001 + 0.009 * torch.rand(N, K // 64, device=dev, generator=gen)).to(torch.bfloat16)
+        b = (-8.0 * s.float()).to(torch.bfloat16)
+        return q, s, b
+
+    # M = 32, K = 8192: the batched GEMV splits K four ways (partials 4*M*N*4 B)
+    M, K = 32, 8192
+    N1, N2 = 2048, 262144            # 1 MiB of partials, then 128 MiB
+    q1, s1, b1 = quant(N1, K)
+    q2, s2, b2 = quant(N2, K)
+    x = (torch.randn(M, K, device=dev, generator=gen)).to(torch.bfloat16)
+    y1 = torch.empty((M, N1), dtype=torch.float32, device=dev)
+    y2 = torch.empty((M, N2), dtype=torch.bfloat16, device=dev)
+
+    def small():
+        ops.gemv4_b(q1, s1, b1, x, y1, N1, K, M)
+
+    small()
+    torch.cuda.synchronize()
+    ref = ops.bits_of(y1).copy()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        small()
+    torch.cuda.synchronize()
+    for r in range(3):
+        y1.zero_()
+        ops.gemv4_b(q2, s2, b2, x, y2, N2, K, M)   # grows the workspace on the first pass
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(ops.bits_of(y1), ref, err_msg=f"replay {r} after growth")
