@@ -150,6 +150,23 @@ int miori_gemm_q4(const void* A, const void* q, const void* scales,
                   const void* biases, void* C, uint32_t M, uint32_t N, uint32_t K,
                   uint32_t group, int out_dtype, miori_stream stream);
 
+/* Size of the fixed scratch array of miori_gemm_q4_static (bytes per GPU). */
+#define MIORI_STATIC_SCRATCH_BYTES (32u << 20)
+
+/* Allocation-free variant of miori_gemm_q4 (no counterpart in the
+ * reference): for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, shape rules and results as miori_gemm_q4, but the split-K
+ * partials go to a fixed per-GPU device array of MIORI_STATIC_SCRATCH_BYTES
+ * instead of the library's growable workspace, so the call never allocates.
+ * A shape whose partials (splits x M x N x 4 bytes) exceed the array returns
+ * MIORI_E_SCRATCH before anything is enqueued. All calls on one GPU share
+ * the array: calls that overlap on one GPU (other streams, other threads)
+ * race, and calls on one stream are ordered. */
+int miori_gemm_q4_static(const void* A, const void* q, const void* scales,
+                         const void* biases, void* C, uint32_t M, uint32_t N, uint32_t K,
+                         uint32_t group, int out_dtype, miori_stream stream);
+
 /* Batch-engine projection policy: C[M][N] = A[M][K] . W^T for 4-bit MLX
  * weights W (q, scales, biases) with an optional bf16 cache of the same W
  * (row-major [N][K], as miori_dequant_q4_tile writes it; NULL if none).

@@ -28,6 +28,7 @@ SIGNATURES = {
     "miori_gemv_q8_batched": ([_P, _P, _P, _P, _P, _U, _U, _U, _U, _I, _P], _I),
     "miori_gemm_bf16": ([_P, _P, _P, _U, _U, _U, _I, _P], _I),
     "miori_gemm_q4": ([_P, _P, _P, _P, _P, _U, _U, _U, _U, _I, _P], _I),
+    "miori_gemm_q4_static": ([_P, _P, _P, _P, _P, _U, _U, _U, _U, _I, _P], _I),
     "miori_linear_q4": ([_P, _P, _P, _P, _P, _P, _U, _U, _U, _U, _I, _P], _I),
     "miori_gemm_naive": ([_P, _P, _P, _U, _U, _U, _U, _U, _U, _P], _I),
     "miori_rmsnorm_gemv_q4": ([_P, _P, ctypes.c_float, _P, _P, _P, _P, _U, _U, _U, _I, _P], _I),

@@ -32,7 +32,7 @@ HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__",
 HOST_LINK = [f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib"]
 
 SOURCES = ["gemv.hip", "skinny.hip", "dequant.hip", "gemm.hip", "naive.hip", "workspace.cpp",
-           "capi.cpp"]
+           "capi.cpp", "noalloc.cpp"]
 
 FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
