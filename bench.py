@@ -324,9 +324,8 @@ def policy_table(c, steps=50):
             rec["exact_us"].append(round(te * 1e3 / steps, 2))
             rec["bf16_cache_us"].append(round(tc * 1e3 / steps, 2))
             rec["fused_us"].append(round(tf * 1e3 / steps, 2))
-        rec["exact_fastest_at_every_M"] = all(
-            e <= min(cc, f) * 1.02 for e, cc, f in zip(rec["exact_us"], rec["bf16_cache_us"],
-                                                         rec["fused_us"]))
+        rec["exact_beats_bf16_cache_at_every_M"] = all(
+            e < cc for e, cc in zip(rec["exact_us"], rec["bf16_cache_us"]))
         out.append(rec)
         print(f"[bench] policy {rec}", file=sys.stderr, flush=True)
         del qs, ss, bs, Bs

@@ -173,10 +173,11 @@ int miori_gemm_q4_static(const void* A, const void* q, const void* scales,
  * Replaces BatchEngine::linear (src/batch.cpp:223-230), which runs the exact
  * 4-bit gemv4_b at <= 4 active slots and otherwise the bf16-cache GEMM
  * (gemm_mpp32 up to 32 rows, gemm_mpp beyond). Here:
- *  - M <= 32: the exact batched 4-bit GEMV (miori_gemv_q4_batched). It reads
- *    a quarter of the bytes of the bf16 cache and is the faster of the two at
- *    every M = 1..32 on the decode projection shapes, so the cache is never
- *    read for decode;
+ *  - M <= 32: the exact batched 4-bit GEMV (miori_gemv_q4_batched), the
+ *    reference's gemv4_b semantics (no bf16 rounding of the weights). It
+ *    reads a quarter of the bytes of the bf16 cache and is faster than the
+ *    cache GEMM at every M = 1..32 on the decode projection shapes (1.3-2.7x),
+ *    so the cache is never read for decode;
  *  - M > 32: miori_gemm_bf16 on the cache when one is given, else the fused
  *    4-bit GEMM (miori_gemm_q4).
  * Shape rules are those of the entry point taken. */
