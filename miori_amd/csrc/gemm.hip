@@ -80,6 +80,85 @@ struct Cfg {
     static_assert(!Q4 || NST == 3, "the fused pipeline is written for three stages");
 };
 
+// Epilogue of one wave's WM x WN accumulator tile, through LDS (the stage
+// buffers are free once every wave is past the main loop; the caller
+// synchronises the workgroup first). Accumulator element e of lane l is row
+// 8*(e/4) + 4*(l/32) + e%4, column l%32 of its 32x32 tile. Each wave writes
+// EPR rows of its fp32 tile at a time to its own LDS region (row stride
+// WN + 8 floats: the two half-waves of a write land on disjoint banks), then
+// reads them back 8 columns per lane and stores 16 bytes (bf16) or 2 x 16
+// bytes (fp32) per lane, or, split-K, the fp32 partial tile to part[ksp].
+// Only this wave touches its region, and a wave's LDS accesses complete in
+// order, so passes need no barrier.
+template <class CF>
+__device__ __forceinline__ void store_wave_tile(f32x16_t (&acc)[CF::TM][CF::TN], uint8_t* lds,
+                                                uint32_t wave, uint32_t lane, uint32_t wm,
+                                                uint32_t wn, uint32_t m0, uint32_t n0, uint32_t M,
+                                                uint32_t N, void* __restrict__ C, int out_bf16,
+                                                float* __restrict__ part, uint32_t ksp,
+                                                uint32_t SK) {
+    constexpr uint32_t RS = CF::WN + 8;  // floats per LDS row
+    constexpr int EPR = CF::EPR;         // rows per pass
+    float* ep = reinterpret_cast<float*>(lds) + wave * (EPR * RS);
+    constexpr uint32_t CPR = CF::WN / 8;          // 8-column chunks per row
+    constexpr uint32_t RPI = 64 / CPR;            // rows per read-back iteration
+    const uint32_t cc = lane % CPR, rr = lane / CPR;
+    const uint32_t col = n0 + wn * CF::WN + cc * 8u;
+    auto store8 = [&](uint32_t row, f32x4_t v0, f32x4_t v1) {
+        if (out_bf16) {
+            u32x4_t o;
+            bf16x2_t p0 = {(__bf16)v0[0], (__bf16)v0[1]}, p1 = {(__bf16)v0[2], (__bf16)v0[3]};
+            bf16x2_t p2 = {(__bf16)v1[0], (__bf16)v1[1]}, p3 = {(__bf16)v1[2], (__bf16)v1[3]};
+            o[0] = __builtin_bit_cast(uint32_t, p0);
+            o[1] = __builtin_bit_cast(uint32_t, p1);
+            o[2] = __builtin_bit_cast(uint32_t, p2);
+            o[3] = __builtin_bit_cast(uint32_t, p3);
+            *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(C) + (size_t)row * N + col) = o;
+        } else {
+            float* dst = reinterpret_cast<float*>(C) + (size_t)row * N + col;
+            *reinterpret_cast<f32x4_t*>(dst) = v0;
+            *reinterpret_cast<f32x4_t*>(dst + 4) = v1;
+        }
+    };
+    static_assert(CF::WM % EPR == 0 && EPR % 32 == 0, "passes cover whole 32-row MFMA tiles");
+#pragma unroll
+    for (int ps = 0; ps < CF::WM / EPR; ++ps) {
+#pragma unroll
+        for (int i = ps * (EPR / 32); i < (ps + 1) * (EPR / 32); ++i)
+#pragma unroll
+            for (int j = 0; j < CF::TN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const uint32_t r = (i - ps * (EPR / 32)) * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                    ep[r * RS + j * 32 + (lane & 31u)] = acc[i][j][e];
+                }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const uint32_t rbase = m0 + wm * CF::WM + ps * EPR;  // first output row of this pass
+        if (SK == 1) {
+#pragma unroll 4
+            for (uint32_t r = rr; r < (uint32_t)EPR; r += RPI) {
+                const uint32_t row = rbase + r;
+                const f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u);
+                const f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u + 4u);
+                if (row < M && col < N) store8(row, v0, v1);
+            }
+        } else {
+            // Split-K: the fp32 partial tile goes to part[ksp]; a second kernel
+            // adds the SK partials in split order (deterministic, and spread
+            // over every CU rather than funnelled through one workgroup per tile).
+            for (uint32_t r = rr; r < (uint32_t)EPR; r += RPI) {
+                const uint32_t row = rbase + r;
+                if (row >= M || col >= N) continue;
+                float* dst = part + ((size_t)ksp * M + row) * N + col;
+                *reinterpret_cast<f32x4_t*>(dst) = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u);
+                *reinterpret_cast<f32x4_t*>(dst + 4) = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u + 4u);
+            }
+        }
+        // the next pass rewrites this region: its reads must have returned
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+}
+
 template <int BM, int BN, bool Q4, int G>
 __global__ __launch_bounds__(256) void gemm_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
@@ -419,75 +498,146 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
 
-    // Epilogue through LDS (the stage buffers are free once every wave is past
-    // the loop). Accumulator element e of lane l is row 8*(e/4) + 4*(l/32) +
-    // e%4, column l%32 of its 32x32 tile. Each wave writes EPR rows of its
-    // WM x WN fp32 tile at a time to its own LDS region (row stride WN + 8
-    // floats: the two half-waves of a write land on disjoint banks), then
-    // reads them back 8 columns per lane and stores 16 bytes (bf16) or
-    // 2 x 16 bytes (fp32) per lane. Only this wave touches its region, and a
-    // wave's LDS accesses complete in order, so passes need no barrier.
     __syncthreads();
-    constexpr uint32_t RS = CF::WN + 8;  // floats per LDS row
-    constexpr int EPR = CF::EPR;         // rows per pass
-    float* ep = reinterpret_cast<float*>(lds) + wave * (EPR * RS);
-    constexpr uint32_t CPR = CF::WN / 8;          // 8-column chunks per row
-    constexpr uint32_t RPI = 64 / CPR;            // rows per read-back iteration
-    const uint32_t cc = lane % CPR, rr = lane / CPR;
-    const uint32_t col = n0 + wn * CF::WN + cc * 8u;
-    auto store8 = [&](uint32_t row, f32x4_t v0, f32x4_t v1) {
-        if (out_bf16) {
-            u32x4_t o;
-            bf16x2_t p0 = {(__bf16)v0[0], (__bf16)v0[1]}, p1 = {(__bf16)v0[2], (__bf16)v0[3]};
-            bf16x2_t p2 = {(__bf16)v1[0], (__bf16)v1[1]}, p3 = {(__bf16)v1[2], (__bf16)v1[3]};
-            o[0] = __builtin_bit_cast(uint32_t, p0);
-            o[1] = __builtin_bit_cast(uint32_t, p1);
-            o[2] = __builtin_bit_cast(uint32_t, p2);
-            o[3] = __builtin_bit_cast(uint32_t, p3);
-            *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(C) + (size_t)row * N + col) = o;
-        } else {
-            float* dst = reinterpret_cast<float*>(C) + (size_t)row * N + col;
-            *reinterpret_cast<f32x4_t*>(dst) = v0;
-            *reinterpret_cast<f32x4_t*>(dst + 4) = v1;
+    store_wave_tile<CF>(acc, lds, wave, lane, wm, wn, m0, n0, M, N, C, out_bf16, part, ksp, SK);
+}
+
+// Producer / consumer form of the bf16 GEMM: eight waves, two per SIMD.
+// Waves 0-3 (consumers, 2x2 grid of (BM/2) x (BN/2) tiles) only read MFMA
+// fragments from LDS and run the MFMAs; waves 4-7 (producers) only issue the
+// global -> LDS DMA of the operand tiles and wait for it. A consumer never
+// waits on vector memory, so while one wave of a SIMD waits for its operand
+// stream the other keeps the matrix core busy. The 3-stage ring and its
+// single barrier per K tile are those of gemm_kernel: at the barrier of tile
+// kt the consumers have read all of tile kt (stage kt % 3 is free) and the
+// producers have waited for tile kt+1; the producers then issue tile kt+3
+// into the freed stage, so two tiles stay in flight behind the one being
+// multiplied. The fragment order, MFMA sequence and epilogue are
+// gemm_kernel's, so both forms give bit-identical results.
+template <int BM, int BN>
+__global__ __launch_bounds__(512) void gemm_pc_kernel(
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
+    uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t tiles_m, int remap,
+    float* __restrict__ part, uint32_t SK, uint32_t ntiles) {
+    using CF = Cfg<BM, BN, false, 64>;
+    static_assert(CF::NST == 3, "the producer / consumer ring has three stages");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[CF::LDS];
+
+    const uint32_t t = threadIdx.x;
+    const uint32_t lane = t & 63u, wave = t >> 6;
+    const bool producer = wave >= 4;
+    const uint32_t w4 = wave & 3u;
+    const uint32_t wm = w4 >> 1, wn = w4 & 1u;
+
+    uint32_t pid = blockIdx.x;
+    const uint32_t nwg = gridDim.x;
+    if (remap && (nwg & 7u) == 0) pid = (pid & 7u) * (nwg >> 3) + (pid >> 3);
+    const uint32_t tile = pid % ntiles, ksp = pid / ntiles;
+    const uint32_t tm = tile % tiles_m, tn = tile / tiles_m;
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t KT_ALL = K / BK;
+    const uint32_t kt0 = KT_ALL * ksp / SK;
+    const uint32_t KT = KT_ALL * (ksp + 1) / SK - kt0;
+
+    f32x16_t acc[CF::TM][CF::TN];
+
+    if (producer) {
+        // Producer wave w4 moves 8-row groups [w4*PA, (w4+1)*PA) of the A tile
+        // and [w4*PB, (w4+1)*PB) of the B tile; one DMA instruction = 8 rows x
+        // 128 bytes, lane -> (row, swizzled 16-byte chunk).
+        constexpr int PA = BM / 32, PB = BN / 32, PL = PA + PB;
+        const uint32_t w4s = __builtin_amdgcn_readfirstlane(w4);
+        uint32_t off[PL];
+#pragma unroll
+        for (int p = 0; p < PL; ++p) {
+            const bool is_a = p < PA;
+            const uint32_t r = (w4 * (is_a ? PA : PB) + (is_a ? p : p - PA)) * 8u + (lane >> 3);
+            const uint32_t kb = (lane & 7u) ^ (r & 7u) ^ ((r >> 3) & 1u);
+            const uint32_t row = is_a ? min(m0 + r, M - 1u) : min(n0 + r, N - 1u);
+            off[p] = row * K * 2u + kb * 16u;
         }
-    };
-    static_assert(CF::WM % EPR == 0 && EPR % 32 == 0, "passes cover whole 32-row MFMA tiles");
+        auto issue = [&](uint32_t kt, uint32_t st) {
 #pragma unroll
-    for (int ps = 0; ps < CF::WM / EPR; ++ps) {
+            for (int p = 0; p < PL; ++p) {
+                const bool is_a = p < PA;
+                const uint32_t r0 = (w4s * (is_a ? PA : PB) + (is_a ? p : p - PA)) * 8u;
+                const uint8_t* base =
+                    reinterpret_cast<const uint8_t*>(is_a ? A : B) + (size_t)(kt0 + kt) * BK * 2u;
+                dma16(base + off[p], lds + (is_a ? CF::A_OFF + st * CF::A_ST
+                                                 : CF::B_OFF + st * CF::B_ST) + r0 * ROWB);
+            }
+        };
+        issue(0, 0);
+        if (KT > 1) issue(1, 1);
+        if (KT > 2) issue(2, 2);
+        if (KT > 2) wait_vm<2 * PL>(); else if (KT > 1) wait_vm<PL>(); else wait_vm<0>();
+        barrier_lds();  // tile 0 has landed
+        for (uint32_t kt = 0; kt + 1 < KT; ++kt) {
+            if (kt + 2 < KT) wait_vm<PL>(); else wait_vm<0>();
+            barrier_lds();  // tile kt+1 has landed; stage kt % 3 is free
+            if (kt + 3 < KT) issue(kt + 3, kt % 3);
+        }
+    } else {
+        __builtin_amdgcn_s_setprio(2);
 #pragma unroll
-        for (int i = ps * (EPR / 32); i < (ps + 1) * (EPR / 32); ++i)
+        for (int i = 0; i < CF::TM; ++i)
 #pragma unroll
             for (int j = 0; j < CF::TN; ++j)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const uint32_t r = (i - ps * (EPR / 32)) * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                    ep[r * RS + j * 32 + (lane & 31u)] = acc[i][j][e];
-                }
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        const uint32_t rbase = m0 + wm * CF::WM + ps * EPR;  // first output row of this pass
-        if (SK == 1) {
-#pragma unroll 4
-            for (uint32_t r = rr; r < (uint32_t)EPR; r += RPI) {
-                const uint32_t row = rbase + r;
-                const f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u);
-                const f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u + 4u);
-                if (row < M && col < N) store8(row, v0, v1);
+                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+        bf16x8_t af[2][CF::TM], bf[2][CF::TN];
+        const uint32_t fsw = (lane & 7u) ^ ((lane >> 3) & 1u);
+        const uint32_t c0 = (4u * (lane >> 5)) ^ fsw;
+        const uint32_t lrow = (lane & 31u) * ROWB;
+        auto read_frags = [&](uint32_t kt, int ks, int slot) {
+            const uint32_t chunk = ((c0 ^ (uint32_t)ks) << 4) + lrow;
+            const uint32_t a_addr = CF::A_OFF + (kt % 3u) * CF::A_ST + wm * CF::WM * ROWB + chunk;
+            const uint32_t b_addr = CF::B_OFF + (kt % 3u) * CF::B_ST + wn * CF::WN * ROWB + chunk;
+#pragma unroll
+            for (int i = 0; i < CF::TM; ++i)
+                asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(af[slot][i]) : "v"(a_addr), "i"(i * 32 * ROWB));
+#pragma unroll
+            for (int j = 0; j < CF::TN; ++j)
+                asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(bf[slot][j]) : "v"(b_addr), "i"(j * 32 * ROWB));
+        };
+        constexpr int NFR = CF::TM + CF::TN;
+        auto mfmas = [&](int slot) {
+#pragma unroll
+            for (int i = 0; i < CF::TM; ++i)
+#pragma unroll
+                for (int j = 0; j < CF::TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][i], bf[slot][j],
+                                                                        acc[i][j], 0, 0, 0);
+        };
+        barrier_lds();  // tile 0 has landed
+        read_frags(0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        for (uint32_t kt = 0; kt < KT; ++kt) {
+#pragma unroll
+            for (int ks = 0; ks < BK / 16 - 1; ++ks) {
+                read_frags(kt, ks + 1, (ks + 1) & 1);
+                asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(NFR) : "memory");  // k-step ks has landed
+                __builtin_amdgcn_sched_barrier(0);
+                mfmas(ks & 1);
+                __builtin_amdgcn_sched_barrier(0);
             }
-        } else {
-            // Split-K: the fp32 partial tile goes to part[ksp]; a second kernel
-            // adds the SK partials in split order (deterministic, and spread
-            // over every CU rather than funnelled through one workgroup per tile).
-            for (uint32_t r = rr; r < (uint32_t)EPR; r += RPI) {
-                const uint32_t row = rbase + r;
-                if (row >= M || col >= N) continue;
-                float* dst = part + ((size_t)ksp * M + row) * N + col;
-                *reinterpret_cast<f32x4_t*>(dst) = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u);
-                *reinterpret_cast<f32x4_t*>(dst + 4) = *reinterpret_cast<const f32x4_t*>(ep + r * RS + cc * 8u + 4u);
+            if (kt + 1 < KT) {
+                barrier_lds();  // completes the last k-step's reads; tile kt+1 has landed
+                read_frags(kt + 1, 0, 0);
+            } else {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             }
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas((BK / 16 - 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        // the next pass rewrites this region: its reads must have returned
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_setprio(0);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    if (!producer)
+        store_wave_tile<CF>(acc, lds, w4, lane, wm, wn, m0, n0, M, N, C, out_bf16, part, ksp, SK);
 }
 
 // out[i] = sum over k = 0..SK-1 of part[k][i], in that order; 8 outputs per
@@ -551,10 +701,23 @@ hipError_t launch_cfg(const void* A, const void* B, const void* q, const void* s
         const hipError_t e = scratch_get(st, (size_t)SK * M * N * 4, &part);
         if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, Q4, G>), dim3(ntiles * SK), dim3(256), 0, st,
-                       (const uint16_t*)A, (const uint16_t*)B, (const uint32_t*)q,
-                       (const uint16_t*)s, (const uint16_t*)b, C, M, N, K, out_bf16, tiles_m,
-                       remap, part, SK, ntiles);
+    static const int pc = tuning_env("MIORI_GEMM_PC", 1);
+    if constexpr (!Q4 && Cfg<BM, BN, false, 64>::NST == 3 && BM * BN >= 128 * 128) {
+        if (pc)
+            hipLaunchKernelGGL((gemm_pc_kernel<BM, BN>), dim3(ntiles * SK), dim3(512), 0, st,
+                               (const uint16_t*)A, (const uint16_t*)B, C, M, N, K, out_bf16,
+                               tiles_m, remap, part, SK, ntiles);
+        else
+            hipLaunchKernelGGL((gemm_kernel<BM, BN, Q4, G>), dim3(ntiles * SK), dim3(256), 0, st,
+                               (const uint16_t*)A, (const uint16_t*)B, (const uint32_t*)q,
+                               (const uint16_t*)s, (const uint16_t*)b, C, M, N, K, out_bf16,
+                               tiles_m, remap, part, SK, ntiles);
+    } else {
+        hipLaunchKernelGGL((gemm_kernel<BM, BN, Q4, G>), dim3(ntiles * SK), dim3(256), 0, st,
+                           (const uint16_t*)A, (const uint16_t*)B, (const uint32_t*)q,
+                           (const uint16_t*)s, (const uint16_t*)b, C, M, N, K, out_bf16, tiles_m,
+                           remap, part, SK, ntiles);
+    }
     if (SK > 1) {
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

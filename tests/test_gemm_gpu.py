@@ -124,3 +124,44 @@ def test_gemm_tile_shape_consistency(dev, m_small, m_big):
     torch.cuda.synchronize()
     np.testing.assert_array_equal(Cs.cpu().numpy(), Cs2.cpu().numpy())
     np.testing.assert_array_equal(Cs.cpu().numpy(), Cb[:m_small].cpu().numpy())
+
+
+_CLASSIC = r"""
+import sys, numpy as np, torch
+sys.path.insert(0, sys.argv[1])
+from miori_amd import ops
+M, N, K = map(int, sys.argv[2:5])
+A = torch.from_numpy(np.load(sys.argv[5])).cuda().view(torch.bfloat16)
+B = torch.from_numpy(np.load(sys.argv[6])).cuda().view(torch.bfloat16)
+C = torch.empty((M, N), dtype=torch.float32, device="cuda")
+ops.gemm_mpp(A, B, C, M, N, K)
+torch.cuda.synchronize()
+np.save(sys.argv[7], C.cpu().numpy())
+"""
+
+
+@pytest.mark.parametrize("M,K,N", [(1024, 2048, 8192), (1472, 2048, 2560), (300, 8192, 2048)])
+def test_gemm_producer_consumer_matches_classic(dev, tmp_path, M, K, N):
+    """The eight-wave producer/consumer bf16 GEMM (the default for 256x128
+    and 128x128 tiles) is bit-identical to the four-wave form
+    (MIORI_GEMM_PC=0, run in a child process: the switch is read once per
+    process)."""
+    import subprocess
+    import sys
+
+    say(f"gemm producer/consumer vs classic M={M} K={K} N={N}")
+    w, Bbits, A = _operands(M, N, K, seed=M + 5 * N, dev=dev)
+    Ad = ops.to_device_bits(A, dev)
+    Bd = ops.to_device_bits(Bbits, dev)
+    C = torch.empty((M, N), dtype=torch.float32, device=dev)
+    ops.gemm_mpp(Ad, Bd, C, M, N, K)
+    torch.cuda.synchronize()
+    fa, fb, fc = tmp_path / "a.npy", tmp_path / "b.npy", tmp_path / "c.npy"
+    np.save(fa, A.view(np.int16))
+    np.save(fb, Bbits.view(np.int16))
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, MIORI_GEMM_PC="0")
+    r = subprocess.run([sys.executable, "-c", _CLASSIC, root, str(M), str(N), str(K), str(fa),
+                        str(fb), str(fc)], env=env, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    np.testing.assert_array_equal(C.cpu().numpy().view(np.uint32), np.load(fc).view(np.uint32))
