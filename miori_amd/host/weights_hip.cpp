@@ -1,9 +1,10 @@
 #include "weights_hip.h"
 
 #include <cctype>
+#include <cerrno>
 #include <cstdio>
 #include <cstring>
-#include <fstream>
+#include <memory>
 #include <stdexcept>
 
 namespace miori {
@@ -168,57 +169,97 @@ Weights::~Weights() {
     }
 }
 
+namespace {
+
+// The safetensors format bounds its JSON header at 100 MB.
+constexpr uint64_t kHeaderCap = 100ull << 20;
+
+struct CloseFile {
+    void operator()(FILE* f) const {
+        if (f) fclose(f);
+    }
+};
+using File = std::unique_ptr<FILE, CloseFile>;
+
+bool read_all(FILE* f, void* dst, uint64_t n) {
+    return n == 0 || fread(dst, 1, (size_t)n, f) == (size_t)n;
+}
+
+}  // namespace
+
+// A safetensors file is <u64 little-endian header size><JSON header><data>.
+// Everything is validated (header bounds, every tensor's byte range) before
+// the data block is read and before any device memory is touched; the
+// object is only modified once the device copy exists.
 bool Weights::load(Metal& m, const std::string& path, std::string& err) {
-    std::ifstream f(path, std::ios::binary);
-    if (!f) { err = "cannot open " + path; return false; }
-    f.seekg(0, std::ios::end);
-    const size_t file_size = (size_t)f.tellg();
-    f.seekg(0, std::ios::beg);
-    uint64_t header_len = 0;
-    f.read((char*)&header_len, 8);
-    if (!f || header_len == 0 || header_len > 16 * 1024 * 1024 || 8 + header_len > file_size) {
-        err = "bad safetensors header length";
+    auto reject = [&](const std::string& why) {
+        err = path + ": " + why;
         return false;
-    }
-    std::string header(header_len, '\0');
-    f.read(header.data(), (std::streamsize)header_len);
-    if (!f) { err = "truncated header"; return false; }
-    const size_t data_start = 8 + (size_t)header_len;
+    };
+    File f(fopen(path.c_str(), "rb"));
+    if (!f) return reject(std::string("open failed: ") + strerror(errno));
+    if (fseeko(f.get(), 0, SEEK_END) != 0) return reject("not a seekable file");
+    const off_t end = ftello(f.get());
+    if (end < 0) return reject("size unknown");
+    const uint64_t total = (uint64_t)end;
+    rewind(f.get());
+
+    uint8_t prefix[8];
+    if (total < 8 || !read_all(f.get(), prefix, 8)) return reject("no 8-byte header size");
+    uint64_t hsize = 0;
+    for (int i = 7; i >= 0; --i) hsize = (hsize << 8) | prefix[i];
+    if (hsize == 0 || hsize > kHeaderCap || hsize > total - 8)
+        return reject("header size " + std::to_string(hsize) + " does not fit a " +
+                      std::to_string(total) + "-byte file");
+    std::string json((size_t)hsize, '\0');
+    if (!read_all(f.get(), &json[0], hsize)) return reject("header cut short");
+
+    std::map<std::string, Tensor> table;
     try {
-        tensors_ = parse_safetensors_header(header);
+        table = parse_safetensors_header(json);
     } catch (const std::exception& e) {
-        err = e.what();
-        return false;
+        return reject(e.what());
     }
-    host_.resize(file_size - data_start);
-    f.read((char*)host_.data(), (std::streamsize)host_.size());
-    if (!f) { err = "truncated data"; return false; }
-    for (auto& kv : tensors_) {
-        Tensor& t = kv.second;
-        if (t.end > host_.size()) { err = "tensor out of range: " + t.name; return false; }
-        t.ptr = host_.data() + t.begin;
-    }
+    const uint64_t data_bytes = total - 8 - hsize;
+    for (const auto& kv : table)
+        if (kv.second.end > data_bytes)
+            return reject("tensor " + kv.first + " ends at byte " + std::to_string(kv.second.end) +
+                          " of a " + std::to_string(data_bytes) + "-byte data block");
+
+    std::vector<uint8_t> data((size_t)data_bytes);
+    if (!read_all(f.get(), data.data(), data_bytes)) return reject("data block cut short");
+    MTL::Buffer* dev = nullptr;
     try {
-        buf_ = m.new_buffer(host_.size(), /*shared=*/false);
-        buf_->upload(host_.data(), host_.size());
+        dev = m.new_buffer(data.empty() ? 1 : data.size(), /*shared=*/false);
+        dev->upload(data.data(), data.size());
     } catch (const std::exception& e) {
-        err = e.what();
-        return false;
+        if (dev) {
+            dev->release();
+            delete dev;
+        }
+        return reject(std::string("device copy failed: ") + e.what());
     }
+    if (buf_) {
+        buf_->release();
+        delete buf_;
+    }
+    buf_ = dev;
+    host_ = std::move(data);
+    tensors_ = std::move(table);
+    for (auto& kv : tensors_) kv.second.ptr = host_.data() + kv.second.begin;
     return true;
 }
 
-const Tensor& Weights::get(const std::string& name) const {
-    auto it = tensors_.find(name);
-    if (it == tensors_.end()) throw std::runtime_error("missing tensor: " + name);
-    return it->second;
-}
-
 const Tensor* Weights::find(const std::string& name) const {
-    auto it = tensors_.find(name);
-    return it == tensors_.end() ? nullptr : &it->second;
+    const auto it = tensors_.find(name);
+    return it != tensors_.end() ? &it->second : nullptr;
 }
 
-bool Weights::has(const std::string& name) const { return tensors_.count(name) != 0; }
+const Tensor& Weights::get(const std::string& name) const {
+    if (const Tensor* t = find(name)) return *t;
+    throw std::runtime_error("weights: no tensor named '" + name + "'");
+}
+
+bool Weights::has(const std::string& name) const { return find(name) != nullptr; }
 
 }  // namespace miori
