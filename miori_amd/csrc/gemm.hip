@@ -47,6 +47,17 @@ __device__ __forceinline__ uint32_t swz(uint32_t r, uint32_t kb) {
     return r * ROWB + ((kb ^ (r & 7u) ^ ((r >> 3) & 1u)) << 4);
 }
 
+// Buffer loads as inline asm (the compiler inserts no waits for them; the
+// caller places s_waitcnt vmcnt by hand and ties the result below it).
+__device__ __forceinline__ void asm_load16(u32x4_t& d, rsrc_t r, uint32_t off) {
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(d) : "v"(off), "s"(r));
+}
+__device__ __forceinline__ void asm_load_u16(uint32_t& d, rsrc_t r, uint32_t off) {
+    asm volatile("buffer_load_ushort %0, %1, %2, 0 offen" : "=v"(d) : "v"(off), "s"(r));
+}
+__device__ __forceinline__ void tie(u32x4_t& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void tie(uint32_t& v) { asm volatile("" : "+v"(v)); }
+
 template <int BM, int BN, bool Q4, int G>
 struct Cfg {
     static constexpr int WM = BM / 2, WN = BN / 2;   // wave tile
@@ -502,25 +513,39 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     store_wave_tile<CF>(acc, lds, wave, lane, wm, wn, m0, n0, M, N, C, out_bf16, part, ksp, SK);
 }
 
-// Producer / consumer form of the bf16 GEMM: eight waves, two per SIMD.
+// Producer / consumer form of the GEMM: eight waves, two per SIMD.
 // Waves 0-3 (consumers, 2x2 grid of (BM/2) x (BN/2) tiles) only read MFMA
-// fragments from LDS and run the MFMAs; waves 4-7 (producers) only issue the
-// global -> LDS DMA of the operand tiles and wait for it. A consumer never
-// waits on vector memory, so while one wave of a SIMD waits for its operand
-// stream the other keeps the matrix core busy. The 3-stage ring and its
-// single barrier per K tile are those of gemm_kernel: at the barrier of tile
-// kt the consumers have read all of tile kt (stage kt % 3 is free) and the
-// producers have waited for tile kt+1; the producers then issue tile kt+3
-// into the freed stage, so two tiles stay in flight behind the one being
-// multiplied. The fragment order, MFMA sequence and epilogue are
-// gemm_kernel's, so both forms give bit-identical results.
-template <int BM, int BN>
+// fragments from LDS and run the MFMAs; waves 4-7 (producers) fill the
+// 3-stage LDS ring. A consumer never waits on vector memory, so while one
+// wave of a SIMD waits for its operands the other keeps the matrix core
+// busy. At the barrier of tile kt the consumers have read all of tile kt
+// (stage kt % 3 is free) and tiles kt+1 and kt+2 are complete in LDS; the
+// producers then fill the freed stage with tile kt+3.
+//  * A (both forms) and bf16 B: global -> LDS DMA, two tiles in flight
+//    behind the one being multiplied.
+//  * Fused 4-bit B (Q4): each producer thread owns one 32-code chunk of the
+//    128 x 64 tile (row t/2, half t%2). Its codes, scale and bias are loaded
+//    into registers one tile before they are needed (buffer loads: rows and
+//    groups past the operand read as zero and are never stored), then
+//    dequantised to bf16_rne(q*s + b) -- the dequant kernels' value -- and
+//    written to the swizzled bf16 B stage with ds_write_b128, while the
+//    consumers multiply. The matrix cores see exactly the operands of the
+//    two-step dequant + bf16 GEMM.
+// Per producer iteration (after the barrier of tile kt): issue A(kt+3) and
+// the codes of tile kt+4; wait for A(kt+2) and the codes of kt+3 (loads
+// complete in issue order); dequantise kt+3 into stage kt % 3; barrier. The
+// fragment order, MFMA sequence and epilogue are gemm_kernel's, so every
+// form gives bit-identical results.
+template <int BM, int BN, bool Q4, int G>
 __global__ __launch_bounds__(512) void gemm_pc_kernel(
-    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
-    uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t tiles_m, int remap,
-    float* __restrict__ part, uint32_t SK, uint32_t ntiles) {
-    using CF = Cfg<BM, BN, false, 64>;
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
+    const uint32_t* __restrict__ q, const uint16_t* __restrict__ s,
+    const uint16_t* __restrict__ bsc, void* __restrict__ C, uint32_t M, uint32_t N,
+    uint32_t K, int out_bf16, uint32_t tiles_m, int remap, float* __restrict__ part,
+    uint32_t SK, uint32_t ntiles) {
+    using CF = Cfg<BM, BN, false, 64>;  // A / B ring and epilogue layout of the bf16 form
     static_assert(CF::NST == 3, "the producer / consumer ring has three stages");
+    static_assert(!Q4 || BN == 128, "fused: one producer thread per 32-code chunk of 128 rows");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[CF::LDS];
 
     const uint32_t t = threadIdx.x;
@@ -542,10 +567,10 @@ __global__ __launch_bounds__(512) void gemm_pc_kernel(
     f32x16_t acc[CF::TM][CF::TN];
 
     if (producer) {
-        // Producer wave w4 moves 8-row groups [w4*PA, (w4+1)*PA) of the A tile
-        // and [w4*PB, (w4+1)*PB) of the B tile; one DMA instruction = 8 rows x
-        // 128 bytes, lane -> (row, swizzled 16-byte chunk).
-        constexpr int PA = BM / 32, PB = BN / 32, PL = PA + PB;
+        // DMA: producer wave w4 moves 8-row groups [w4*PA, (w4+1)*PA) of the A
+        // tile (and, bf16 B, [w4*PB, (w4+1)*PB) of the B tile); one
+        // instruction = 8 rows x 128 bytes, lane -> (row, swizzled chunk).
+        constexpr int PA = BM / 32, PB = Q4 ? 0 : BN / 32, PL = PA + PB;
         const uint32_t w4s = __builtin_amdgcn_readfirstlane(w4);
         uint32_t off[PL];
 #pragma unroll
@@ -567,15 +592,144 @@ __global__ __launch_bounds__(512) void gemm_pc_kernel(
                                                  : CF::B_OFF + st * CF::B_ST) + r0 * ROWB);
             }
         };
-        issue(0, 0);
-        if (KT > 1) issue(1, 1);
-        if (KT > 2) issue(2, 2);
-        if (KT > 2) wait_vm<2 * PL>(); else if (KT > 1) wait_vm<PL>(); else wait_vm<0>();
-        barrier_lds();  // tile 0 has landed
-        for (uint32_t kt = 0; kt + 1 < KT; ++kt) {
-            if (kt + 2 < KT) wait_vm<PL>(); else wait_vm<0>();
-            barrier_lds();  // tile kt+1 has landed; stage kt % 3 is free
-            if (kt + 3 < KT) issue(kt + 3, kt % 3);
+        if constexpr (!Q4) {
+            issue(0, 0);
+            if (KT > 1) issue(1, 1);
+            if (KT > 2) issue(2, 2);
+            if (KT > 2) wait_vm<2 * PL>(); else if (KT > 1) wait_vm<PL>(); else wait_vm<0>();
+            barrier_lds();  // tile 0 has landed
+            for (uint32_t kt = 0; kt + 1 < KT; ++kt) {
+                if (kt + 2 < KT) wait_vm<PL>(); else wait_vm<0>();
+                barrier_lds();  // tile kt+1 has landed; stage kt % 3 is free
+                if (kt + 3 < KT) issue(kt + 3, kt % 3);
+            }
+        } else {
+            // This thread's chunk: row r of the tile, codes [32c, 32c + 32) of
+            // each 64-wide K tile.
+            const uint32_t pt = w4 * 64u + lane;
+            const uint32_t r = pt >> 1, c = pt & 1u;
+            const uint32_t row = n0 + r;  // rows >= N read zeros (never stored)
+            const uint32_t ng = K / G;
+            const rsrc_t rq = make_rsrc(q, N * (K / 2u));
+            const rsrc_t rs = make_rsrc(s, N * ng * 2u);
+            const rsrc_t rb = make_rsrc(bsc, N * ng * 2u);
+            const uint32_t qrow = row < N ? row * (K / 2u) + c * 16u : kOOB;
+            const uint32_t srow = row < N ? row * ng * 2u : kOOB;
+            struct Codes {
+                u32x4_t raw;
+                uint32_t sc, bi;
+            };
+            // The loads are inline asm, invisible to the compiler's own vmcnt
+            // waits (which would otherwise drain every load before the first
+            // use of a register loaded two iterations earlier); they are
+            // waited for by hand, and tie() keeps every use below the wait.
+            auto fetch = [&](uint32_t kt, Codes& x) {
+                const uint32_t kg = (kt0 + kt) * BK + c * 32u;  // first code of the chunk
+                const uint32_t so = srow == kOOB ? kOOB : srow + (kg / G) * 2u;
+                asm_load16(x.raw, rq, qrow == kOOB ? kOOB : qrow + (kt0 + kt) * (BK / 2u));
+                asm_load_u16(x.sc, rs, so);
+                asm_load_u16(x.bi, rb, so);
+            };
+            auto settle = [](Codes& x) {
+                tie(x.raw);
+                tie(x.sc);
+                tie(x.bi);
+            };
+            // bf16_rne(q*s + b) of the 32 codes into B stage st, row r,
+            // 16-byte chunks 4c .. 4c+3 (swizzled like the DMA'd bf16 tiles)
+            auto dequant = [&](const Codes& x, uint32_t st) {
+                const float sc = bf16_bits_to_f32(x.sc), bi = bf16_bits_to_f32(x.bi);
+                uint8_t* dst = lds + CF::B_OFF + st * CF::B_ST;
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    const uint32_t v = x.raw[w];
+                    uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
+                    // opaque to the compiler, so byte j converts with one
+                    // v_cvt_f32_ubyte<j> instead of a bit-field extract + convert
+                    tie(lo);
+                    tie(hi);
+                    u32x4_t o;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float f0 = fmaf((float)((lo >> (8 * j)) & 0xFFu), sc, bi);
+                        const float f1 = fmaf((float)((hi >> (8 * j)) & 0xFFu), sc, bi);
+                        bf16x2_t pr = {(__bf16)f0, (__bf16)f1};
+                        o[j] = __builtin_bit_cast(uint32_t, pr);
+                    }
+                    *reinterpret_cast<u32x4_t*>(dst + swz(r, c * 4u + w)) = o;
+                }
+            };
+            constexpr int PQ = 3;  // vector loads per fetch
+            // Issue order per iteration: codes(kt+5), then A(kt+3). The codes
+            // of a tile are dequantised two iterations after they were
+            // issued, right after the barrier, without waiting for the A
+            // tile issued in between; the wait for A(kt+2) follows.
+            // prologue: codes(0..4) and A(0..2) in the steady-state order
+            // (codes(j+5) before A(j+3)); dequantise tiles 0..2
+            auto cl = [&](uint32_t kt) { return kt < KT ? kt : KT - 1u; };  // clamped tile
+            Codes x0, x1, x2, x3, x4;
+            fetch(0, x0);
+            fetch(cl(1), x1);
+            fetch(cl(2), x2);
+            issue(0, 0);
+            fetch(cl(3), x3);
+            if (KT > 1) issue(1, 1);
+            fetch(cl(4), x4);
+            if (KT > 2) issue(2, 2);
+            wait_vm<0>();
+            settle(x0);
+            settle(x1);
+            settle(x2);
+            settle(x3);
+            settle(x4);
+            dequant(x0, 0);
+            if (KT > 1) dequant(x1, 1);
+            if (KT > 2) dequant(x2, 2);
+            barrier_lds();  // tiles 0..2 are in LDS
+            // Steady state, after the barrier of tile kt (stage kt % 3 free):
+            // cur = codes(kt+3), codes(kt+4) in flight, fx receives
+            // codes(kt+5). Three code sets rotate (step kt dequantises
+            // R[kt % 3] and refills R[(kt + 2) % 3], whose tile was
+            // dequantised a step earlier); the loop body has no branches, so
+            // no register is reused while a load is still filling it.
+            auto step = [&](uint32_t kt, Codes& cur, Codes& fx) {
+                wait_vm<PQ + PL>();  // codes(kt+3); codes(kt+4) and A(kt+2) may be in flight
+                settle(cur);
+                dequant(cur, kt % 3);
+                fetch(cl(kt + 5), fx);
+                issue(kt + 3, kt % 3);
+                wait_vm<PQ + PL>();  // A(kt+2) has landed
+            };
+            uint32_t kt = 0;
+            for (; kt + 5 < KT; kt += 3) {  // steps kt .. kt+2 all fetch a real tile
+                barrier_lds();
+                step(kt, x3, x2);
+                barrier_lds();
+                step(kt + 1, x4, x3);
+                barrier_lds();
+                step(kt + 2, x2, x4);
+            }
+            // Tail: no more fetches; x3 / x4 hold codes(kt+3) / codes(kt+4).
+            wait_vm<0>();
+            settle(x3);
+            settle(x4);
+            if (kt + 1 < KT) {
+                barrier_lds();
+                if (kt + 3 < KT) {
+                    dequant(x3, kt % 3);
+                    issue(kt + 3, kt % 3);
+                }
+                wait_vm<0>();
+            }
+            if (kt + 2 < KT) {
+                barrier_lds();
+                if (kt + 4 < KT) {
+                    dequant(x4, (kt + 1) % 3);
+                    issue(kt + 4, (kt + 1) % 3);
+                }
+                wait_vm<0>();
+            }
+            for (kt += 2; kt + 1 < KT; ++kt) barrier_lds();
         }
     } else {
         __builtin_amdgcn_s_setprio(2);
@@ -702,10 +856,11 @@ hipError_t launch_cfg(const void* A, const void* B, const void* q, const void* s
         if (e != hipSuccess) return e;
     }
     static const int pc = tuning_env("MIORI_GEMM_PC", 1);
-    if constexpr (!Q4 && Cfg<BM, BN, false, 64>::NST == 3 && BM * BN >= 128 * 128) {
+    if constexpr (Cfg<BM, BN, false, 64>::NST == 3 && BM * BN >= 128 * 128) {
         if (pc)
-            hipLaunchKernelGGL((gemm_pc_kernel<BM, BN>), dim3(ntiles * SK), dim3(512), 0, st,
-                               (const uint16_t*)A, (const uint16_t*)B, C, M, N, K, out_bf16,
+            hipLaunchKernelGGL((gemm_pc_kernel<BM, BN, Q4, G>), dim3(ntiles * SK), dim3(512), 0,
+                               st, (const uint16_t*)A, (const uint16_t*)B, (const uint32_t*)q,
+                               (const uint16_t*)s, (const uint16_t*)b, C, M, N, K, out_bf16,
                                tiles_m, remap, part, SK, ntiles);
         else
             hipLaunchKernelGGL((gemm_kernel<BM, BN, Q4, G>), dim3(ntiles * SK), dim3(256), 0, st,

@@ -76,6 +76,13 @@ def test_gemm_kernel_waits(tmp_path):
     bad = {k: v for k, v in res.items() if v}
     assert not bad, {k[:80]: v[:3] for k, v in bad.items()}
     assert not _spilled(text, "gemm_kernel")
+    # the producer / consumer form (bf16 and fused 4-bit; inline-asm code
+    # loads in the fused producers)
+    res = check_file(text, "gemm_pc_kernel")
+    assert len(res) == 8, "expected every gemm_pc_kernel instantiation"
+    bad = {k: v for k, v in res.items() if v}
+    assert not bad, {k[:80]: v[:3] for k, v in bad.items()}
+    assert not _spilled(text, "gemm_pc_kernel")
 
 
 @pytest.mark.skipif(not shutil.which(HIPCC) and not os.path.exists(HIPCC), reason="hipcc not available")
