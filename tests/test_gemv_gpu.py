@@ -36,6 +36,8 @@ def _run(lin, x_dev, M, out_dtype):
     (33, 4096, 128, torch.bfloat16),    # ragged N, group 128
     (7, 16384, 64, torch.float32),      # 2 chunks per lane
     (5, 32768, 64, torch.float32),      # largest K
+    (33, 2048, 64, torch.bfloat16),     # lane-exchanged scales, ragged last block
+    (1001, 1024, 32, torch.float32),    # lane-exchanged scales, two dwords per lane
 ])
 def test_gemv4_parity(dev, N, K, G, odt):
     say(f"gemv4 N={N} K={K} G={G} out={odt}")
