@@ -77,6 +77,11 @@ def _parse():
     p.add_argument("--quick", action="store_true",
                    help="headline, GEMM and config rows only (no policy table, no chain)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    p.add_argument("--headline-only", action="store_true",
+                   help="only the config-0 GEMV and the launch floors (for counter passes)")
+    p.add_argument("--case", default=None,
+                   help="time one case only, KIND,M,N,K with KIND gemv4 | gemv8 | gemm_bf16 | "
+                        "gemm_q4 (for profiling runs)")
     p.add_argument("--calib-copy", action="store_true",
                    help="also run a 256 MiB device copy (reference for the HBM byte counters)")
     return p.parse_args()
@@ -391,6 +396,16 @@ def launch_floors(c, nbytes, steps):
             "torch_copy_same_bytes_us": round(t_copy * 1e3 / steps, 3)}
 
 
+def calib_copy(torch, dev):
+    """A plain 256 MiB device copy, three times: it reads and writes exactly
+    256 MiB per launch, the reference for scaling FETCH_SIZE / WRITE_SIZE."""
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
 # ---------------------------------------------------------------- CPU baselines
 def _timed(fn, budget):
     """Run fn() at least once and until `budget` seconds; seconds per call."""
@@ -479,9 +494,25 @@ def main():
         print(f"[bench] {row}", file=sys.stderr, flush=True)
         return row
 
+    if args.case:
+        kind, M, N, K = args.case.split(",")
+        M, N, K = int(M), int(N), int(K)
+        if kind in ("gemv4", "gemv8"):
+            row = gemv_row(c, 4 if kind == "gemv4" else 8, M, N, K)
+        elif kind in ("gemm_bf16", "gemm_q4"):
+            row = gemm_row(c, M, N, K, kind == "gemm_q4", steps=min(args.steps, 30))
+        else:
+            raise SystemExit(f"unknown case kind {kind}")
+        print(json.dumps(row), flush=True)
+        return
     head = log(gemv_row(c, 4, 1, 8192, 2048, hot=True, tag="gemv4"))
-    gemm = log(gemm_row(c, 1024, 8192, 2048, False, steps=min(args.steps, 100), vendor=True))
     floors = launch_floors(c, head["bytes"], args.steps)
+    if args.headline_only:
+        if args.calib_copy:
+            calib_copy(torch, dev)
+        print(json.dumps({"gemv4": head, "gemv_floors": floors}), flush=True)
+        return
+    gemm = log(gemm_row(c, 1024, 8192, 2048, False, steps=min(args.steps, 100), vendor=True))
 
     rows = [dict(config=0, **head)]
     for K, N in [(2048, 8192), (2048, 2048), (2048, 512), (8192, 2048)]:
@@ -522,11 +553,7 @@ def main():
             if same:
                 r["cpu_baseline"] = base
     if args.calib_copy:
-        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
+        calib_copy(torch, dev)
 
     wbytes_head = head["bytes"] - 2048 * 2 - 8192 * 2
     out = {

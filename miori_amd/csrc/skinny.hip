@@ -25,10 +25,11 @@
 //    words between lane quarters with v_permlane32/16_swap (group 32: a 4x4
 //    word transpose; group 64 and 8-bit: one 32-lane swap; group >= 128:
 //    none), and x fragments are loaded at the matching k (kmap below).
-//  * Exact modes: codes become exact bf16 integers (128+q via one AND-OR per
-//    code pair), each group is accumulated alone (D_g) with X_g = sum of x
-//    over the group from an MFMA against ones, and folded in fp32:
-//        acc += s*D_g + (b - 128 s) X_g        (8-bit: hi nibbles x16, 2176)
+//  * Exact modes: codes become exact bf16 integers (4-bit: 128+q via one
+//    AND-OR per code pair; 8-bit: q itself, byte convert + pack), each group
+//    is accumulated alone (D_g) with X_g = sum of x over the group from an
+//    MFMA against ones, and folded in fp32:
+//        acc += s*D_g + (b - 128 s) X_g        (8-bit: acc += s*D_g + b X_g)
 //    so the dequantised weights are never rounded.
 //  * Q4F and BF16 run the identical MFMA sequence (same k order, same
 //    accumulation order), so the fused product is bit-identical to
@@ -112,8 +113,8 @@ __device__ __forceinline__ bf16x8_t as_bf16x8_u(uint32_t a, uint32_t b, uint32_t
 }
 
 // x fragment: 8 consecutive bf16, pair-permuted to the slot order of the
-// weight fragment (4-bit exact: (x0,x4)(x1,x5)(x2,x6)(x3,x7); 8-bit exact:
-// (x0,x2)(x1,x3)(x4,x6)(x5,x7); Q4F / BF16: natural order).
+// weight fragment (4-bit exact: (x0,x4)(x1,x5)(x2,x6)(x3,x7); 8-bit exact,
+// Q4F, BF16: natural order).
 template <int MODE>
 __device__ __forceinline__ bf16x8_t x_frag(u32x4_t d) {
     if constexpr (MODE == Q4X)
@@ -121,11 +122,6 @@ __device__ __forceinline__ bf16x8_t x_frag(u32x4_t d) {
                            __builtin_amdgcn_perm(d[2], d[0], 0x07060302u),
                            __builtin_amdgcn_perm(d[3], d[1], 0x05040100u),
                            __builtin_amdgcn_perm(d[3], d[1], 0x07060302u));
-    else if constexpr (MODE == Q8X)
-        return as_bf16x8_u(__builtin_amdgcn_perm(d[1], d[0], 0x05040100u),
-                           __builtin_amdgcn_perm(d[1], d[0], 0x07060302u),
-                           __builtin_amdgcn_perm(d[3], d[2], 0x05040100u),
-                           __builtin_amdgcn_perm(d[3], d[2], 0x07060302u));
     else
         return __builtin_bit_cast(bf16x8_t, d);
 }
@@ -186,6 +182,23 @@ __device__ __forceinline__ NibConst nib_const() {
     return k;
 }
 __device__ __forceinline__ uint32_t nib2(uint32_t v, NibConst k) { return (v & k.m) | k.c; }
+
+// Eight 8-bit codes (bytes of a then b, k order) as bf16: every integer
+// 0..255 is exact in bf16, so convert + pack loses nothing. The bytes are
+// made opaque first so each converts with one v_cvt_f32_ubyte<i>.
+__device__ __forceinline__ bf16x8_t codes8_bf16(uint32_t a, uint32_t b) {
+    asm volatile("" : "+v"(a), "+v"(b));
+    u32x4_t o;
+    const uint32_t w[2] = {a, b};
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        bf16x2_t p0 = {(__bf16)(float)(w[h] & 0xFFu), (__bf16)(float)((w[h] >> 8) & 0xFFu)};
+        bf16x2_t p1 = {(__bf16)(float)((w[h] >> 16) & 0xFFu), (__bf16)(float)(w[h] >> 24)};
+        o[2 * h] = __builtin_bit_cast(uint32_t, p0);
+        o[2 * h + 1] = __builtin_bit_cast(uint32_t, p1);
+    }
+    return __builtin_bit_cast(bf16x8_t, o);
+}
 
 __device__ __forceinline__ f32x4_t mfma16(bf16x8_t a, bf16x8_t b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -383,12 +396,9 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
                 const uint32_t wv[4] = {w0, w1, w2, w3};
 #pragma unroll
                 for (int f = 0; f < NF; ++f) {
-                    f32x4_t dd[MT], dh[MT];
+                    f32x4_t dd[MT];
 #pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) {
-                        dd[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-                        dh[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-                    }
+                    for (int mt = 0; mt < MT; ++mt) dd[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                     for (int r = f * C::SPF; r < (f + 1) * C::SPF; ++r) {
                         if constexpr (MODE == Q4X) {
@@ -400,34 +410,23 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
 #pragma unroll
                             for (int mt = 0; mt < MT; ++mt) dd[mt] = mfma16(xf[mt][r], bfr, dd[mt]);
                         } else {
-                            const uint32_t vx = wv[2 * r], vy = wv[2 * r + 1];
-                            const bf16x8_t blo = as_bf16x8_u(nib2(vx, nk),
-                                                             nib2(vx >> 8, nk),
-                                                             nib2(vy, nk),
-                                                             nib2(vy >> 8, nk));
-                            const bf16x8_t bhi = as_bf16x8_u(nib2(vx >> 4, nk),
-                                                             nib2(vx >> 12, nk),
-                                                             nib2(vy >> 4, nk),
-                                                             nib2(vy >> 12, nk));
+                            // 8 codes in k order; a code (0..255) is an exact bf16
+                            const bf16x8_t bq = codes8_bf16(wv[2 * r], wv[2 * r + 1]);
 #pragma unroll
-                            for (int mt = 0; mt < MT; ++mt) {
-                                dd[mt] = mfma16(xf[mt][r], blo, dd[mt]);
-                                dh[mt] = mfma16(xf[mt][r], bhi, dh[mt]);
-                            }
+                            for (int mt = 0; mt < MT; ++mt) dd[mt] = mfma16(xf[mt][r], bq, dd[mt]);
                         }
                     }
                     const int d = (i * C::KB + f * C::SPF * 32) / G;
                     const float sv = s_of(nt, d), bv = b_of(nt, d);
                     const float sc = valid ? sv : 0.f;
                     const float bi = valid ? bv : 0.f;
-                    const float bx = (MODE == Q4X) ? fmaf(-128.f, sc, bi) : fmaf(-2176.f, sc, bi);
+                    // 4-bit codes carry the +128 of the bf16 trick
+                    const float bx = (MODE == Q4X) ? fmaf(-128.f, sc, bi) : bi;
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const float v = (MODE == Q4X) ? dd[mt][e] : fmaf(16.f, dh[mt][e], dd[mt][e]);
-                            acc[nt][mt][e] = fmaf(sc, v, fmaf(bx, dx[f][mt][e], acc[nt][mt][e]));
-                        }
+                        for (int e = 0; e < 4; ++e)
+                            acc[nt][mt][e] = fmaf(sc, dd[mt][e], fmaf(bx, dx[f][mt][e], acc[nt][mt][e]));
                 }
             }
         }
