@@ -5,6 +5,7 @@
 // shim above it turns a non-zero status into std::runtime_error, the error
 // convention of the reference's Metal::pso (src/metal.cpp:31-37).
 #include "../../include/miori_hip.h"
+#include "common.hpp"
 #include "kernels.hpp"
 
 #include <hip/hip_runtime.h>
@@ -51,7 +52,10 @@ hipError_t launch_batched(int bits, const void* q, const void* s, const void* b,
                           const void* x, void* y, uint32_t M, uint32_t N, uint32_t K,
                           uint32_t G, int out_bf16, hipStream_t st) {
     const int mode = bits == 4 ? 0 : 1;
-    if (M > 4 && skinny_ok(mode, M, N, K, G, s, b))
+    // MIORI_BATCH_MFMA_MIN_M overrides the first M served by the MFMA kernel
+    // (tuning sweeps; default 5)
+    static const uint32_t min_m = (uint32_t)tuning_env("MIORI_BATCH_MFMA_MIN_M", 5);
+    if (M >= min_m && skinny_ok(mode, M, N, K, G, s, b))
         return launch_skinny(mode, x, q, s, b, y, M, N, K, G, out_bf16, st);
     return launch_gemv_valu(bits, q, s, b, x, y, M, N, K, G, out_bf16, st);
 }
