@@ -48,6 +48,8 @@ def test_reference_test_gemm(dev):
     (17, 257, 100, 104, 100, 260),      # 32-row tile, ragged and strided
     (8, 600, 2048, 2048, 2048, 600),    # 8-row tile (M <= 8)
     (3, 300, 90, 96, 90, 300),          # 8-row tile, ragged K and strides (element loads)
+    (12, 300, 90, 96, 90, 300),         # 16x256 tile, element loads (K % 8 != 0)
+    (5, 20, 100, 104, 100, 20),         # 16x16 tile (N <= 32), element loads
 ])
 def test_naive_shapes_bit_exact(dev, M, N, K, lda, ldb, ldc):
     say(f"gemm_naive M={M} N={N} K={K} lda={lda} ldb={ldb} ldc={ldc}")
