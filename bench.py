@@ -421,57 +421,75 @@ def _timed(fn, budget):
 
 
 def cpu_baselines(synth, budget=2.5):
-    """The oracle, single-threaded, on a bounded sample of each config's
-    workload, scaled to the GPU row's unit. Returns {config: baseline}."""
+    """The oracle on a bounded sample of each config's workload, scaled to
+    the GPU row's unit: single-threaded (the reference's faithful check
+    loop, `cores` = 1) and, under `threaded`, the same loop split over the
+    host's cores with OpenMP. Returns {config: baseline}."""
     import numpy as np
 
     import oracle
 
+    nt = min(16, os.cpu_count() or 1)
     out = {}
+
+    def pair(fn, fn_mt, scale, unit, work, sample, b=budget):
+        per, n = _timed(fn, b)
+        per_mt, n_mt = _timed(fn_mt, b / 4)
+        full, full_mt = per * scale, per_mt * scale
+        return {"value": round(work / full, 6), "unit": unit, "cores": 1, "kind": "port",
+                "us": round(full * 1e6, 1),
+                "sample": sample.format(n=n, ms=per * 1e3),
+                "threaded": {"value": round(work / full_mt, 6), "cores": nt,
+                             "us": round(full_mt * 1e6, 1),
+                             "sample": f"{n_mt} passes of the same sample, OpenMP over {nt} "
+                                       f"threads, {per_mt * 1e3:.1f} ms each"}}
+
     # config 0: full 8192 x 2048 g64 4-bit GEMV, M = 1 (src/main.cpp:73-84)
     w = synth.quant_weights(8192, 2048, 64, 4, seed=synth.BASE_SEED + 401)
     x = synth.activations(1, 2048)
-    per, n = _timed(lambda: oracle.gemv_f64(w.q, w.s, w.b, x, 4, 2048, 64, nthreads=1), budget * 2)
-    out[0] = {"value": round((w.nbytes + 4096 + 16384) / per / 1e9, 4), "unit": "GB/s",
-              "cores": 1, "kind": "port", "us": round(per * 1e6, 1),
-              "sample": f"{n} full passes of the 8192x2048 g64 4-bit GEMV (M=1), per-element "
-                        f"dequant + fp64 accumulate, {per * 1e3:.1f} ms/pass"}
+    out[0] = pair(lambda: oracle.gemv_f64(w.q, w.s, w.b, x, 4, 2048, 64, nthreads=1),
+                  lambda: oracle.gemv_f64(w.q, w.s, w.b, x, 4, 2048, 64, nthreads=nt),
+                  1, "GB/s", (w.nbytes + 4096 + 16384) / 1e9,
+                  "{n} full passes of the 8192x2048 g64 4-bit GEMV (M=1), per-element dequant "
+                  "+ fp64 accumulate, {ms:.1f} ms/pass", budget * 2)
     # config 1: gate/up 2048 -> 8192 at M = 8, rows [0, 1024) extrapolated to 8192
     x8 = synth.activations(8, 2048)
-    per, n = _timed(lambda: oracle.gemv_rows_f64(w.q, w.s, w.b, x8, 4, 2048, 64, 0, 1024), budget)
-    full = per * 8
-    nb = w.nbytes + 8 * 4096 + 8 * 8192 * 2
-    out[1] = {"value": round(nb / full / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-              "us": round(full * 1e6, 1),
-              "sample": f"{n} passes over output rows 0..1023 of the 2048->8192 g64 GEMV at "
-                        f"M=8, {per * 1e3:.1f} ms each, x8 extrapolated to all 8192 rows"}
-    # config 2: 8-bit lm_head M = 1, rows [0, 2048) extrapolated to 131072
+    out[1] = pair(lambda: oracle.gemv_rows_f64(w.q, w.s, w.b, x8, 4, 2048, 64, 0, 1024),
+                  lambda: oracle.gemv_rows_f64(w.q, w.s, w.b, x8, 4, 2048, 64, 0, 1024,
+                                               nthreads=nt),
+                  8, "GB/s", (w.nbytes + 8 * 4096 + 8 * 8192 * 2) / 1e9,
+                  "{n} passes over output rows 0..1023 of the 2048->8192 g64 GEMV at M=8, "
+                  "{ms:.1f} ms each, x8 extrapolated to all 8192 rows")
+    # config 2: 8-bit lm_head M = 1, a 2048-row slice extrapolated to 131072
     w8 = synth.quant_weights(2048, 2048, 64, 8, seed=synth.BASE_SEED + 402)
-    per, n = _timed(lambda: oracle.gemv_f64(w8.q, w8.s, w8.b, x, 8, 2048, 64, nthreads=1), budget)
-    full = per * 64
-    nb = 131072 * (2048 + 2 * 32 * 2) + 4096 + 131072 * 2
-    out[2] = {"value": round(nb / full / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-              "us": round(full * 1e6, 1),
-              "sample": f"{n} passes of a 2048-row slice of the 8-bit g64 lm_head (M=1), "
-                        f"{per * 1e3:.1f} ms each, x64 extrapolated to 131072 rows"}
+    out[2] = pair(lambda: oracle.gemv_f64(w8.q, w8.s, w8.b, x, 8, 2048, 64, nthreads=1),
+                  lambda: oracle.gemv_f64(w8.q, w8.s, w8.b, x, 8, 2048, 64, nthreads=nt),
+                  64, "GB/s", (131072 * (2048 + 2 * 32 * 2) + 4096 + 131072 * 2) / 1e9,
+                  "{n} passes of a 2048-row slice of the 8-bit g64 lm_head (M=1), {ms:.1f} ms "
+                  "each, x64 extrapolated to 131072 rows")
     # configs 3 / 4: M=1024, K=2048, N=8192; 16 rows of A, extrapolated to 1024
     A = synth.activations(16, 2048)
     Bq = synth.quant_weights(8192, 2048, 64, 4, seed=synth.BASE_SEED + 403)
     Bb = oracle.dequant_bf16(Bq.q, Bq.s, Bq.b, 4, 2048, 64)
     rows = np.arange(16, dtype=np.int64)
-    per, n = _timed(lambda: oracle.gemm_bf16_f64(A, Bb, rows, nthreads=1), budget)
-    full = per * 64
-    flops = 2.0 * 1024 * 8192 * 2048
-    out[3] = {"value": round(flops / full / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
-              "kind": "port", "us": round(full * 1e6, 1),
-              "sample": f"{n} passes of 16 rows x 8192 x 2048 (src/main.cpp:594-601 loop, "
-                        f"fp64 accumulate), {per * 1e3:.0f} ms each, x64 extrapolated to M=1024"}
+    tflop = 2.0 * 1024 * 8192 * 2048 / 1e12
+    out[3] = pair(lambda: oracle.gemm_bf16_f64(A, Bb, rows, nthreads=1),
+                  lambda: oracle.gemm_bf16_f64(A, Bb, rows, nthreads=nt),
+                  64, "TFLOP/s", tflop,
+                  "{n} passes of 16 rows x 8192 x 2048 (src/main.cpp:594-601 loop, fp64 "
+                  "accumulate), {ms:.0f} ms each, x64 extrapolated to M=1024")
     per_d, nd = _timed(lambda: oracle.dequant_bf16(Bq.q, Bq.s, Bq.b, 4, 2048, 64), budget / 2)
-    full4 = per_d + per * 64
-    out[4] = {"value": round(flops / full4 / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
-              "kind": "port", "us": round(full4 * 1e6, 1),
+    c3 = out[3]
+    full4 = per_d + c3["us"] * 1e-6
+    full4_mt = per_d + c3["threaded"]["us"] * 1e-6
+    out[4] = {"value": round(tflop / full4, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+              "us": round(full4 * 1e6, 1),
               "sample": f"dequant of the 8192x2048 g64 weights ({per_d * 1e3:.0f} ms, {nd} "
-                        f"passes) + the config-3 GEMM sample above, for one M=1024 projection"}
+                        "passes) + the config-3 GEMM sample, for one M=1024 projection",
+              "threaded": {"value": round(tflop / full4_mt, 6), "cores": nt,
+                           "us": round(full4_mt * 1e6, 1),
+                           "sample": "the same dequant (single thread) + the threaded GEMM "
+                                     "sample"}}
     return out
 
 
