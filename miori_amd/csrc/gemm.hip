@@ -934,10 +934,13 @@ hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* 
                        const void* b, void* C, uint32_t M, uint32_t N, uint32_t K,
                        uint32_t G, int out_bf16, hipStream_t st) {
     // Tile choice (MIORI_GEMM_TILE overrides: 0 = 256x128, 1 = 128x128,
-    // 2 = 256x256, 3 = 64x128, 4 = 64x64):
+    // 2 = 256x256, 3 = 64x128, 4 = 64x64, 5 = 192x256):
     //  * bf16 weight cache: 256x256 tiles (128 flop per operand byte, against
     //    85 for 256x128) once they fill at least 3/4 of the 256 CUs in a
     //    round; the split-K cost model is not applied to them (SK = 1).
+    //    192x256 replaces them when its grid needs fewer rounds at 3/4 the
+    //    cost per round: M=1472, N=8192, K=2048 62.7 -> 56.5 us, K=8192
+    //    220 -> 194 us.
     //  * small grids (K <= 4096, at most 512 64x64 tiles): 64x64 tiles (bf16)
     //    or 64x128 (fused 4-bit), 2-3 workgroups per CU. Both paths take the
     //    K split the cost model picks for the 64x128 grid (usually none), so
@@ -952,12 +955,17 @@ hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* 
     const uint64_t huge = (uint64_t)((M + 255) / 256) * ((N + 255) / 256);
     const uint64_t t64 = (uint64_t)((M + 63) / 64) * ((N + 63) / 64);
     int tile = pick_tile_256x128(M, N, K);
-    if (!q && huge >= 192) tile = 2;
-    else if (K <= 4096 && t64 <= 512) tile = q ? 3 : 4;
+    if (!q && huge >= 192) {
+        // M=1472, N=8192: 8 x 32 = 256 192x256 tiles in one round, against
+        // 6 x 32 = 192 256x256 tiles that leave a quarter of the CUs idle
+        const uint64_t t192 = (uint64_t)((M + 191) / 192) * ((N + 255) / 256);
+        tile = (t192 + 255) / 256 * 3 < (huge + 255) / 256 * 4 ? 5 : 2;
+    } else if (K <= 4096 && t64 <= 512) tile = q ? 3 : 4;
     static const int e_tile = tuning_env("MIORI_GEMM_TILE", -1);
     if (e_tile >= 0) tile = e_tile;
     if (tile == 2 && !q) return launch_cfg<256, 256, false, 64>(A, B, q, s, b, C, M, N, K, out_bf16, 1, st);
-    if (tile == 2) tile = pick_tile_256x128(M, N, K);  // fused: no 256x256 variant
+    if (tile == 5 && !q) return launch_cfg<192, 256, false, 64>(A, B, q, s, b, C, M, N, K, out_bf16, 1, st);
+    if (tile == 2 || tile == 5) tile = pick_tile_256x128(M, N, K);  // fused: no 256x256 variant
     // (64x64 splits as the 64x128 grid, the fused path's tile)
     const uint32_t tbm = tile == 0 ? 256 : (tile == 3 || tile == 4) ? 64 : 128;
     const uint32_t tbn = 128;

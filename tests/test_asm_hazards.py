@@ -72,7 +72,7 @@ def _spilled(text, name):
 def test_gemm_kernel_waits(tmp_path):
     text = _compile("gemm.hip", tmp_path / "gemm.s")
     res = check_file(text, "gemm_kernel")
-    assert len(res) == 14, "expected every gemm_kernel instantiation"
+    assert len(res) == 15, "expected every gemm_kernel instantiation"
     bad = {k: v for k, v in res.items() if v}
     assert not bad, {k[:80]: v[:3] for k, v in bad.items()}
     assert not _spilled(text, "gemm_kernel")

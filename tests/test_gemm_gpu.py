@@ -63,6 +63,7 @@ def _rows_for(M):
     (256, 2048, 2560), (1024, 2048, 2560), (1472, 2048, 2560),
     (1, 64, 16), (23, 128, 80), (300, 192, 144), (64, 2048, 6144),
     (1500, 2048, 8208),                                                  # ragged 256x256 tiles
+    (1400, 2048, 8000),                                                  # ragged 192x256 tiles
     (32, 2048, 2048), (17, 512, 96), (8, 2560, 256), (32, 8192, 512),   # skinny path
 ])
 def test_gemm_bf16_parity(dev, M, K, N):
@@ -80,7 +81,8 @@ def test_gemm_bf16_parity(dev, M, K, N):
 
 @pytest.mark.parametrize("M,K,N,G", [
     (1024, 2048, 8192, 64), (1472, 8192, 2048, 64), (256, 2048, 2560, 64),
-    (1472, 2048, 8192, 64), (1500, 2048, 8208, 64),   # bf16 side on 256x256 tiles
+    (1472, 2048, 8192, 64), (1500, 2048, 8208, 64),   # bf16 side on 192x256 / 256x256 tiles
+    (1400, 2048, 8000, 64),
     (32, 2048, 2048, 64), (32, 8192, 2048, 64), (100, 256, 48, 32), (64, 512, 128, 128),
     (32, 2048, 8192, 64), (9, 1024, 80, 32), (20, 2048, 512, 128),      # skinny path
 ])
