@@ -41,6 +41,7 @@
 
 #include <algorithm>
 #include <type_traits>
+#include <utility>
 
 namespace miori {
 
@@ -51,6 +52,11 @@ constexpr int NW = 8;  // waves per workgroup (widest form; exact modes also use
 
 template <int N>
 using ic = std::integral_constant<int, N>;
+// f(ic<I>) for each I of the sequence, in order
+template <int... I, class F>
+__device__ __forceinline__ void each(std::integer_sequence<int, I...>, F&& f) {
+    (f(ic<I>{}), ...);
+}
 
 template <int MODE, int MT, int NT, int G, int NBW, int NWV>
 struct Sk {
@@ -510,6 +516,217 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
     }
 }
 
+// Persistent 8-bit exact kernel for vocabulary-sized N and 9 <= M <= 32 (the
+// batched lm_head): one workgroup of eight waves per CU stages x (M x K bf16)
+// in LDS once, and every wave then streams whole 16-row tiles of W over the
+// full K, tile w, w + W, w + 2W, ... of the grid's W waves. A wave keeps
+// DEPTH (16 or 32) 64-k blocks of its weight stream in flight, across tile
+// boundaries, and needs no cross-wave reduction: each tile's 16 x M outputs
+// are stored by the wave that computed them. The per-block arithmetic is the
+// skinny kernel's Q8X mode (codes as exact bf16 integers, D_g and X_g by
+// MFMA, acc += s*D_g + b*X_g), with the k order of its lane quarters.
+//  * x is loaded once per CU instead of once per 64 rows, so the vector
+//    memory path carries only the weight stream. Measured at N = 131072,
+//    K = 2048 against the four-wave skinny form (us): M=32 81.9 -> 73.2,
+//    M=24 78.7 -> 71.0, M=17 75.6 -> 67.5, M=16 67.9 -> 64.2, M=9 63.6 ->
+//    63.2. Up to M = 8 the skinny form with x in LDS stays faster (M=8
+//    60.6 against 62.6), and four waves per workgroup were slower than
+//    eight (M=32 82.6: one wave per SIMD serialises its VALU and MFMA work).
+//  * A tile's scales and biases (16 rows x K/G, contiguous) are DMA'd into a
+//    per-wave LDS double buffer just before the tile's first weight load,
+//    one 1 KiB chunk per instruction, so the wait for that block covers them;
+//    the buffer's previous tile is finished by then because a tile has at
+//    least DEPTH blocks. (Loading them per block with the weights, 2-byte
+//    loads from 16 rows, took 93 us at M = 32.)
+//  * Requires G in {64, 128}, K / 64 a power of two >= DEPTH, and the x tile
+//    (16*MT rows of 2K bytes) plus the scale buffers within 160 KiB.
+template <int MT, int G, int DEPTH, int NWV>
+__global__ __launch_bounds__(NWV * 64) void lmh_kernel(const uint16_t* __restrict__ X,
+                                                  const uint8_t* __restrict__ W,
+                                                  const uint16_t* __restrict__ S,
+                                                  const uint16_t* __restrict__ Bi,
+                                                  void* __restrict__ Y, uint32_t M, uint32_t N,
+                                                  uint32_t K, int out_bf16) {
+    constexpr int KB = 64;
+    static_assert(G == 64 || G == 128, "one scale / bias per 64-k block");
+    extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
+    const uint32_t t = threadIdx.x, lane = t & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const uint32_t j = lane & 15u, c = lane >> 4;
+    const uint32_t XR = K * 2u;  // LDS row stride (bytes)
+    const uint32_t rows = min(M, 16u * MT);
+    const uint32_t ng = K / G;
+    const uint32_t sbc = (32u * ng + 1023u) / 1024u;  // 1 KiB chunks per scale tile
+    // this wave's scale / bias buffers: [buffer][s, b][sbc KiB]
+    uint8_t* sbw = xs + 16u * MT * XR + wave * (4u * sbc * 1024u);
+
+    // x rows 0 .. rows-1 into LDS, one 1 KiB DMA per (row, 512-k chunk).
+    // The 16-byte chunk q of row r sits at chunk q ^ (r & 15) of the row, so
+    // the 16 rows of an MFMA fragment read fall on distinct banks; the DMA
+    // writes lanes in order, so each lane fetches the chunk its slot holds.
+    const uint32_t nch = K / 512u;
+    for (uint32_t u = wave; u < rows * nch; u += NWV) {
+        const uint32_t r = u / nch, ch = u % nch;
+        dma16(X + (size_t)r * K + (ch * 64u + (lane ^ (r & 15u))) * 8u, xs + r * XR + ch * 1024u);
+    }
+
+    const uint32_t nbpt = K / KB;  // blocks per tile (a power of two, >= DEPTH)
+    const uint32_t lg = 31u - __builtin_clz(nbpt);
+    const uint32_t ntiles = (N + 15u) / 16u;
+    const uint32_t nw = gridDim.x * NWV, w = blockIdx.x * NWV + wave;
+    const uint32_t T = w < ntiles ? (ntiles - 1u - w) / nw + 1u : 0u;
+    const uint32_t total = T << lg;  // blocks in this wave's stream
+    // scale / bias tile of tile ti into buffer ti % 2 (sources clamped inside
+    // the arrays; rows past N are never stored)
+    const size_t sb_total = (size_t)N * ng * 2u;
+    auto issue_sb = [&](uint32_t ti) {
+        const size_t base = (size_t)min((w + ti * nw) * 16u, N - 1u) * ng * 2u;
+        uint8_t* dst = sbw + (ti & 1u) * (2u * sbc * 1024u);
+        for (uint32_t q = 0; q < sbc; ++q) {
+            const size_t off = min(base + q * 1024u + lane * 16u, sb_total - 16u);
+            dma16(reinterpret_cast<const uint8_t*>(S) + off, dst + q * 1024u);
+            dma16(reinterpret_cast<const uint8_t*>(Bi) + off, dst + (sbc + q) * 1024u);
+        }
+    };
+    if (T > 0) issue_sb(0);
+    wait_vm<0>();
+    barrier_lds();
+    if (T == 0) return;
+
+    u32x4_t wr[DEPTH];
+    // block b of the stream (clamped to the last one: blocks past the end
+    // are loaded and never used)
+    auto issue = [&](uint32_t b, auto sl_c) {
+        constexpr int sl = decltype(sl_c)::value;
+        b = min(b, total - 1u);
+        const uint32_t ti = b >> lg, kb = b & (nbpt - 1u);
+        const uint32_t n = min((w + ti * nw) * 16u + j, N - 1u);
+        ld16(wr[sl], W + (size_t)n * K + kb * KB + 16u * c);
+    };
+    typedef __attribute__((address_space(3))) const u32x4_t* lds_v4;
+    typedef __attribute__((address_space(3))) const uint16_t* lds_u16;
+    uint32_t xoff[MT], xsw[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const uint32_t r = min(mt * 16u + j, rows - 1u);
+        xoff[mt] = r * XR;
+        xsw[mt] = r & 15u;
+    }
+    const bf16x8_t ones = as_bf16x8_u(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+    f32x4_t acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](uint32_t b, auto sl_c) {
+        constexpr int sl = decltype(sl_c)::value;
+        const uint32_t kb = b & (nbpt - 1u);
+        bf16x8_t xf[MT][2];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+                xf[mt][r] = __builtin_bit_cast(
+                    bf16x8_t,
+                    *(lds_v4)(xs + xoff[mt] + ((((kb * KB + kmap<Q8X, G>(c, r)) >> 3) ^ xsw[mt]) << 4)));
+        const uint8_t* sbb = sbw + ((b >> lg) & 1u) * (2u * sbc * 1024u);
+        const uint32_t gi = j * ng + kb * KB / G;
+        const float sc = bf16_bits_to_f32(((lds_u16)sbb)[gi]);
+        const float bi = bf16_bits_to_f32(((lds_u16)(sbb + sbc * 1024u))[gi]);
+        uint32_t w0 = wr[sl][0], w1 = wr[sl][1], w2 = wr[sl][2], w3 = wr[sl][3];
+        swap32u(w0, w2);
+        swap32u(w1, w3);
+        const bf16x8_t q0 = codes8_bf16(w0, w1), q1 = codes8_bf16(w2, w3);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            f32x4_t dx = mfma16(xf[mt][0], ones, f32x4_t{0.f, 0.f, 0.f, 0.f});
+            dx = mfma16(xf[mt][1], ones, dx);
+            f32x4_t dd = mfma16(xf[mt][0], q0, f32x4_t{0.f, 0.f, 0.f, 0.f});
+            dd = mfma16(xf[mt][1], q1, dd);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[mt][e] = fmaf(sc, dd[e], fmaf(bi, dx[e], acc[mt][e]));
+        }
+    };
+    // one block: wait until only the blocks issued after it are in flight
+    // (DEPTH-1 weight loads, plus at most the next tile's scale DMAs, which
+    // are younger), compute it, refill its slot with block b + DEPTH
+    auto step = [&](uint32_t b, auto sl_c) {
+        constexpr int sl = decltype(sl_c)::value;
+        wait_vm<DEPTH - 1>();
+        tie(wr[sl]);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(b, sl_c);
+        // (b is a multiple of DEPTH here, and DEPTH divides a tile's blocks)
+        if constexpr (sl == 0) {
+            const uint32_t tn = (b + DEPTH) >> lg;
+            if (((b + DEPTH) & (nbpt - 1u)) == 0 && tn < T) issue_sb(tn);
+        }
+        issue(b + DEPTH, sl_c);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    const bool bf = out_bf16 != 0;
+    each(std::make_integer_sequence<int, DEPTH>{}, [&](auto i) { issue(decltype(i)::value, i); });
+    for (uint32_t b0 = 0; b0 < total; b0 += DEPTH) {
+        // at a tile's first block: the next tile's scales into the other
+        // buffer (its previous tile is done)
+        each(std::make_integer_sequence<int, DEPTH>{},
+             [&](auto i) { step(b0 + decltype(i)::value, i); });
+        if (((b0 + DEPTH) & (nbpt - 1u)) == 0) {
+            // tile done: rows 4c + e of each m-tile, column j
+            const uint32_t n = (w + (b0 >> lg) * nw) * 16u + j;
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t m = mt * 16u + 4u * c + e;
+                    if (m < M && n < N) store_out(Y, (size_t)m * N + n, acc[mt][e], bf);
+                }
+                acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    }
+    // the last DEPTH issues fill slots that are never read
+    wait_vm<0>();
+    each(std::make_integer_sequence<int, DEPTH>{}, [&](auto i) { tie(wr[decltype(i)::value]); });
+}
+
+// x tile plus the waves' double-buffered scale / bias tiles
+inline size_t lmh_lds_bytes(int mt, uint32_t K, uint32_t G, int nwv) {
+    const size_t sbc = (32u * (K / G) + 1023u) / 1024u;
+    return (size_t)16 * mt * 2u * K + (size_t)nwv * 4 * sbc * 1024;
+}
+
+template <int MT, int G, int DEPTH, int NWV>
+hipError_t launch_lmh(const void* X, const void* W, const void* S, const void* B, void* Y,
+                      uint32_t M, uint32_t N, uint32_t K, int out_bf16, hipStream_t st) {
+    static int cus[64] = {0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    if (cus[dev] == 0) {
+        int n = 0;
+        e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        cus[dev] = n;
+    }
+    const size_t lds = lmh_lds_bytes(MT, K, G, NWV);
+    // (dynamic LDS above 64 KiB is opted into once per device, up to the
+    // whole 160 KiB)
+    static bool attr[64] = {false};
+    if (!attr[dev]) {
+        e = hipFuncSetAttribute((const void*)lmh_kernel<MT, G, DEPTH, NWV>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return e;
+        attr[dev] = true;
+    }
+    const uint32_t ntiles = (N + 15u) / 16u;
+    const uint32_t grid = std::min<uint32_t>((uint32_t)cus[dev], (ntiles + NWV - 1u) / NWV);
+    hipLaunchKernelGGL((lmh_kernel<MT, G, DEPTH, NWV>), dim3(grid), dim3(NWV * 64), lds, st,
+                       (const uint16_t*)X, (const uint8_t*)W, (const uint16_t*)S,
+                       (const uint16_t*)B, Y, M, N, K, out_bf16);
+    return hipGetLastError();
+}
+
 template <int MODE, int MT, int NT, int G, int NBW, int NWV>
 hipError_t launch_sk(const void* X, const void* W, const void* S, const void* B, void* Y,
                      uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t SK,
@@ -631,6 +848,29 @@ hipError_t by_shape(uint32_t G, const void* X, const void* W, const void* S, con
     // which needs whole 512-element chunks of 16-byte aligned rows.
     const bool nw4_ok = sk == 1 && K / kb <= 32 &&
                         (MODE != Q8X || M > 8 || K > 2048 || (K % 512 == 0 && ((uintptr_t)X & 15) == 0));
+    // 8-bit, M > 8 at vocabulary-sized N: the persistent form with x in LDS
+    static const int e_lmh = tuning_env("MIORI_SKINNY_LMH", 1);
+    if constexpr (MODE == Q8X) {
+        const uint32_t nbpt = K / 64u;
+        const bool lmh_ok = e_lmh && M > 8 && N >= 32768 && (G == 64 || G == 128) &&
+                            nbpt >= 16 && (nbpt & (nbpt - 1u)) == 0 &&
+                            lmh_lds_bytes(M > 16 ? 2 : 1, K, G, 8) <= 160u * 1024u &&
+                            ((uintptr_t)X & 15) == 0 && e_nt < 0 && e_nw < 0;
+        if (lmh_ok) {
+            // 32 blocks in flight per wave from K = 2048, else 16
+            const int sel = (M > 16 ? 4 : 0) + (G == 64 ? 0 : 2) + (nbpt >= 32 ? 1 : 0);
+            switch (sel) {
+                case 0: return launch_lmh<1, 64, 16, 8>(X, W, S, B, Y, M, N, K, out_bf16, st);
+                case 1: return launch_lmh<1, 64, 32, 8>(X, W, S, B, Y, M, N, K, out_bf16, st);
+                case 2: return launch_lmh<1, 128, 16, 8>(X, W, S, B, Y, M, N, K, out_bf16, st);
+                case 3: return launch_lmh<1, 128, 32, 8>(X, W, S, B, Y, M, N, K, out_bf16, st);
+                case 4: return launch_lmh<2, 64, 16, 8>(X, W, S, B, Y, M, N, K, out_bf16, st);
+                case 5: return launch_lmh<2, 64, 32, 8>(X, W, S, B, Y, M, N, K, out_bf16, st);
+                case 6: return launch_lmh<2, 128, 16, 8>(X, W, S, B, Y, M, N, K, out_bf16, st);
+                default: return launch_lmh<2, 128, 32, 8>(X, W, S, B, Y, M, N, K, out_bf16, st);
+            }
+        }
+    }
     int nw = 8;
     if ((MODE == Q4X || MODE == Q8X) && N >= 32768 && nw4_ok && e_nt < 0)
         nw = 4;

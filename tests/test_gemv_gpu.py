@@ -201,6 +201,23 @@ def test_batched_skinny_four_wave(dev, bits, M, N, K, G):
     check_close(y, ref, f"gemv{bits}_b four-wave M={M} G={G}")
 
 
+@pytest.mark.parametrize("M,N,K,G", [
+    (9, 40008, 1024, 128), (16, 32768, 2048, 128), (12, 32768, 4096, 128),
+    (17, 32784, 2048, 64), (32, 50000, 1024, 64),
+])
+def test_gemv8_batched_persistent(dev, M, N, K, G):
+    """8-bit, 9 <= M <= 32 at vocabulary-sized N: the persistent form (x in
+    LDS once per CU, whole 16-row tiles over the full K per wave), with ragged
+    N, one and two m-tiles, 16 to 64 blocks per tile and 16 or 32 of them in
+    flight."""
+    say(f"gemv8_b persistent M={M} N={N} K={K} G={G}")
+    w, lin = weights(N, K, G, 8, seed=M * 5 + N, dev=dev)
+    x, xd = acts(M, K, seed=M + 950, dev=dev)
+    y = _run(lin, xd, M, torch.bfloat16)
+    ref = oracle.gemv_f64(w.q, w.s, w.b, x, 8, K, G, nthreads=NT)
+    check_close(y, ref, f"gemv8_b persistent M={M} N={N} K={K}")
+
+
 def test_gemv8_batched_lds_x_fallback(dev):
     """Up to M = 8 the 8-bit vocabulary-sized form stages x in LDS in whole
     512-element chunks; K = 1280 takes the eight-wave form instead, with the
