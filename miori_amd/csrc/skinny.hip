@@ -158,6 +158,11 @@ __device__ __forceinline__ void ldw(u32x4_t& d, const void* p) {
     else
         ld16(d, p);
 }
+// (16 bytes at p + OFF, the offset in the instruction's immediate field)
+template <int OFF>
+__device__ __forceinline__ void ld16_at(u32x4_t& d, const void* p) {
+    asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(d) : "v"(p), "i"(OFF));
+}
 __device__ __forceinline__ void ld8(u32x2_t& d, const void* p) {
     asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(d) : "v"(p));
 }
@@ -527,11 +532,13 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
 // MFMA, acc += s*D_g + b*X_g), with the k order of its lane quarters.
 //  * x is loaded once per CU instead of once per 64 rows, so the vector
 //    memory path carries only the weight stream. Measured at N = 131072,
-//    K = 2048 against the four-wave skinny form (us): M=32 81.9 -> 73.2,
-//    M=24 78.7 -> 71.0, M=17 75.6 -> 67.5, M=16 67.9 -> 64.2, M=9 63.6 ->
-//    63.2. Up to M = 8 the skinny form with x in LDS stays faster (M=8
-//    60.6 against 62.6), and four waves per workgroup were slower than
-//    eight (M=32 82.6: one wave per SIMD serialises its VALU and MFMA work).
+//    K = 2048 against the four-wave skinny form (us): M=32 81.7 -> 68.1,
+//    M=24 78.3 -> 67.1, M=17 75.1 -> 65.1, M=16 67.8 -> 59.8, M=9 63.5 ->
+//    58.5. Four waves per workgroup were slower than eight (M=32 82.6: one
+//    wave per SIMD serialises its VALU and MFMA work), and so was the same
+//    loop with per-block address arithmetic instead of per-chunk bases with
+//    immediate offsets (73.2: 30% more VALU instructions).
+//    Up to M = 8 the skinny form with x in LDS stays the faster one.
 //  * A tile's scales and biases (16 rows x K/G, contiguous) are DMA'd into a
 //    per-wave LDS double buffer just before the tile's first weight load,
 //    one 1 KiB chunk per instruction, so the wait for that block covers them;
@@ -594,45 +601,54 @@ __global__ __launch_bounds__(NWV * 64) void lmh_kernel(const uint16_t* __restric
     if (T == 0) return;
 
     u32x4_t wr[DEPTH];
-    // block b of the stream (clamped to the last one: blocks past the end
-    // are loaded and never used)
-    auto issue = [&](uint32_t b, auto sl_c) {
-        constexpr int sl = decltype(sl_c)::value;
-        b = min(b, total - 1u);
-        const uint32_t ti = b >> lg, kb = b & (nbpt - 1u);
+    // The stream moves in chunks of DEPTH blocks, each inside one tile
+    // (DEPTH divides a tile's blocks). Per chunk the weight, x and scale
+    // addresses are computed once; block i of the chunk adds a compile-time
+    // offset (the load's and the LDS reads' immediate fields).
+    // weight base of the chunk starting at block bn (past the stream's end:
+    // the last tile again, loaded and never used)
+    auto wbase = [&](uint32_t bn) {
+        const uint32_t ti = min(bn >> lg, T - 1u), kb = bn & (nbpt - 1u);
         const uint32_t n = min((w + ti * nw) * 16u + j, N - 1u);
-        ld16(wr[sl], W + (size_t)n * K + kb * KB + 16u * c);
+        return W + (size_t)n * K + kb * KB + 16u * c;
+    };
+    auto issue = [&](const uint8_t* base, auto i_c) {
+        constexpr int i = decltype(i_c)::value;
+        ld16_at<i * KB>(wr[i], base);
     };
     typedef __attribute__((address_space(3))) const u32x4_t* lds_v4;
     typedef __attribute__((address_space(3))) const uint16_t* lds_u16;
-    uint32_t xoff[MT], xsw[MT];
+    // x fragment (m-tile mt, step r) of block i of a chunk at k-block kb0 (a
+    // multiple of 16): row chunk ((kb0 + i) * 8 + k8) ^ sw with sw < 16, which
+    // is kb0 * 8 + (i / 2) * 16 + (((i % 2) * 8 + k8) ^ sw)
+    uint32_t xa[MT][2][2];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-        const uint32_t r = min(mt * 16u + j, rows - 1u);
-        xoff[mt] = r * XR;
-        xsw[mt] = r & 15u;
+        const uint32_t r = min(mt * 16u + j, rows - 1u), sw = r & 15u;
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int p = 0; p < 2; ++p)
+                xa[mt][q][p] = r * XR + ((((uint32_t)p * 8u + kmap<Q8X, G>(c, q) / 8u) ^ sw) << 4);
     }
     const bf16x8_t ones = as_bf16x8_u(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
     f32x4_t acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    auto compute = [&](uint32_t b, auto sl_c) {
-        constexpr int sl = decltype(sl_c)::value;
-        const uint32_t kb = b & (nbpt - 1u);
+    // block i of the chunk: xc = x tile + kb0 * 128 bytes, sc_b / bi_b = this
+    // lane's scale / bias row at the chunk's first group
+    auto compute = [&](const uint8_t* xc, lds_u16 sc_b, lds_u16 bi_b, auto i_c) {
+        constexpr int i = decltype(i_c)::value;
         bf16x8_t xf[MT][2];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int r = 0; r < 2; ++r)
-                xf[mt][r] = __builtin_bit_cast(
-                    bf16x8_t,
-                    *(lds_v4)(xs + xoff[mt] + ((((kb * KB + kmap<Q8X, G>(c, r)) >> 3) ^ xsw[mt]) << 4)));
-        const uint8_t* sbb = sbw + ((b >> lg) & 1u) * (2u * sbc * 1024u);
-        const uint32_t gi = j * ng + kb * KB / G;
-        const float sc = bf16_bits_to_f32(((lds_u16)sbb)[gi]);
-        const float bi = bf16_bits_to_f32(((lds_u16)(sbb + sbc * 1024u))[gi]);
-        uint32_t w0 = wr[sl][0], w1 = wr[sl][1], w2 = wr[sl][2], w3 = wr[sl][3];
+            for (int q = 0; q < 2; ++q)
+                xf[mt][q] = __builtin_bit_cast(bf16x8_t, *(lds_v4)(xc + (i / 2) * 256 + xa[mt][q][i % 2]));
+        const float sc = bf16_bits_to_f32(sc_b[i * KB / G]);
+        const float bi = bf16_bits_to_f32(bi_b[i * KB / G]);
+        uint32_t w0 = wr[i][0], w1 = wr[i][1], w2 = wr[i][2], w3 = wr[i][3];
         swap32u(w0, w2);
         swap32u(w1, w3);
         const bf16x8_t q0 = codes8_bf16(w0, w1), q1 = codes8_bf16(w2, w3);
@@ -646,31 +662,36 @@ __global__ __launch_bounds__(NWV * 64) void lmh_kernel(const uint16_t* __restric
             for (int e = 0; e < 4; ++e) acc[mt][e] = fmaf(sc, dd[e], fmaf(bi, dx[e], acc[mt][e]));
         }
     };
-    // one block: wait until only the blocks issued after it are in flight
-    // (DEPTH-1 weight loads, plus at most the next tile's scale DMAs, which
-    // are younger), compute it, refill its slot with block b + DEPTH
-    auto step = [&](uint32_t b, auto sl_c) {
-        constexpr int sl = decltype(sl_c)::value;
-        wait_vm<DEPTH - 1>();
-        tie(wr[sl]);
-        __builtin_amdgcn_sched_barrier(0);
-        compute(b, sl_c);
-        // (b is a multiple of DEPTH here, and DEPTH divides a tile's blocks)
-        if constexpr (sl == 0) {
-            const uint32_t tn = (b + DEPTH) >> lg;
-            if (((b + DEPTH) & (nbpt - 1u)) == 0 && tn < T) issue_sb(tn);
-        }
-        issue(b + DEPTH, sl_c);
-        __builtin_amdgcn_sched_barrier(0);
-    };
     const bool bf = out_bf16 != 0;
-    each(std::make_integer_sequence<int, DEPTH>{}, [&](auto i) { issue(decltype(i)::value, i); });
+    {
+        const uint8_t* base = wbase(0);
+        each(std::make_integer_sequence<int, DEPTH>{}, [&](auto i) { issue(base, i); });
+    }
     for (uint32_t b0 = 0; b0 < total; b0 += DEPTH) {
-        // at a tile's first block: the next tile's scales into the other
-        // buffer (its previous tile is done)
-        each(std::make_integer_sequence<int, DEPTH>{},
-             [&](auto i) { step(b0 + decltype(i)::value, i); });
-        if (((b0 + DEPTH) & (nbpt - 1u)) == 0) {
+        const uint32_t kb0 = b0 & (nbpt - 1u), bn = b0 + DEPTH;
+        const uint8_t* xc = xs + kb0 * (KB * 2u);
+        const uint8_t* sbb = sbw + ((b0 >> lg) & 1u) * (2u * sbc * 1024u);
+        const lds_u16 sc_b = (lds_u16)sbb + j * ng + kb0 * KB / G;
+        const lds_u16 bi_b = (lds_u16)(sbb + sbc * 1024u) + j * ng + kb0 * KB / G;
+        const uint8_t* nb = wbase(bn);
+        // one block: wait until only the blocks issued after it are in flight
+        // (DEPTH-1 weight loads, plus at most the next tile's scale DMAs,
+        // which are younger), compute it, refill its slot with the block
+        // DEPTH later; at the chunk's first block, when that later chunk
+        // starts a tile, its scales go first, into the other buffer (whose
+        // tile is done)
+        each(std::make_integer_sequence<int, DEPTH>{}, [&](auto i_c) {
+            constexpr int i = decltype(i_c)::value;
+            wait_vm<DEPTH - 1>();
+            tie(wr[i]);
+            __builtin_amdgcn_sched_barrier(0);
+            compute(xc, sc_b, bi_b, i_c);
+            if constexpr (i == 0)
+                if ((bn & (nbpt - 1u)) == 0 && (bn >> lg) < T) issue_sb(bn >> lg);
+            issue(nb, i_c);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        if ((bn & (nbpt - 1u)) == 0) {
             // tile done: rows 4c + e of each m-tile, column j
             const uint32_t n = (w + (b0 >> lg) * nw) * 16u + j;
 #pragma unroll
