@@ -521,6 +521,8 @@ def main():
             row = gemm_row(c, M, N, K, kind == "gemm_q4", steps=min(args.steps, 30))
         else:
             raise SystemExit(f"unknown case kind {kind}")
+        if args.calib_copy:
+            calib_copy(torch, dev)
         print(json.dumps(row), flush=True)
         return
     head = log(gemv_row(c, 4, 1, 8192, 2048, hot=True, tag="gemv4"))

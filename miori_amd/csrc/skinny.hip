@@ -158,11 +158,15 @@ __device__ __forceinline__ void ldw(u32x4_t& d, const void* p) {
     else
         ld16(d, p);
 }
-// (16 bytes at p + OFF, the offset in the instruction's immediate field)
+// (16 bytes at byte offset off + OFF of a buffer, OFF in the instruction's
+// immediate field)
 template <int OFF>
-__device__ __forceinline__ void ld16_at(u32x4_t& d, const void* p) {
-    asm volatile("global_load_dwordx4 %0, %1, off offset:%2" : "=v"(d) : "v"(p), "i"(OFF));
+__device__ __forceinline__ void buf16_at(u32x4_t& d, rsrc_t r, uint32_t off) {
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3" : "=v"(d) : "v"(off), "s"(r), "i"(OFF));
 }
+// an offset past any buffer of the persistent kernel (N * K < 2^31) even
+// with the largest immediate added
+constexpr uint32_t kLmhOOB = 0x80000000u;
 __device__ __forceinline__ void ld8(u32x2_t& d, const void* p) {
     asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(d) : "v"(p));
 }
@@ -605,16 +609,18 @@ __global__ __launch_bounds__(NWV * 64) void lmh_kernel(const uint16_t* __restric
     // (DEPTH divides a tile's blocks). Per chunk the weight, x and scale
     // addresses are computed once; block i of the chunk adds a compile-time
     // offset (the load's and the LDS reads' immediate fields).
-    // weight base of the chunk starting at block bn (past the stream's end:
-    // the last tile again, loaded and never used)
+    // weight offset of the chunk starting at block bn
+    // (a chunk past the stream's end loads through an out-of-range offset:
+    // zeros, counted by vmcnt like any load, with no memory traffic)
+    const rsrc_t rw = make_rsrc(W, N * K);
     auto wbase = [&](uint32_t bn) {
-        const uint32_t ti = min(bn >> lg, T - 1u), kb = bn & (nbpt - 1u);
+        const uint32_t ti = bn >> lg, kb = bn & (nbpt - 1u);
         const uint32_t n = min((w + ti * nw) * 16u + j, N - 1u);
-        return W + (size_t)n * K + kb * KB + 16u * c;
+        return bn < total ? n * K + kb * KB + 16u * c : kLmhOOB;
     };
-    auto issue = [&](const uint8_t* base, auto i_c) {
+    auto issue = [&](uint32_t base, auto i_c) {
         constexpr int i = decltype(i_c)::value;
-        ld16_at<i * KB>(wr[i], base);
+        buf16_at<i * KB>(wr[i], rw, base);
     };
     typedef __attribute__((address_space(3))) const u32x4_t* lds_v4;
     typedef __attribute__((address_space(3))) const uint16_t* lds_u16;
@@ -664,7 +670,7 @@ __global__ __launch_bounds__(NWV * 64) void lmh_kernel(const uint16_t* __restric
     };
     const bool bf = out_bf16 != 0;
     {
-        const uint8_t* base = wbase(0);
+        const uint32_t base = wbase(0);
         each(std::make_integer_sequence<int, DEPTH>{}, [&](auto i) { issue(base, i); });
     }
     for (uint32_t b0 = 0; b0 < total; b0 += DEPTH) {
@@ -673,7 +679,7 @@ __global__ __launch_bounds__(NWV * 64) void lmh_kernel(const uint16_t* __restric
         const uint8_t* sbb = sbw + ((b0 >> lg) & 1u) * (2u * sbc * 1024u);
         const lds_u16 sc_b = (lds_u16)sbb + j * ng + kb0 * KB / G;
         const lds_u16 bi_b = (lds_u16)(sbb + sbc * 1024u) + j * ng + kb0 * KB / G;
-        const uint8_t* nb = wbase(bn);
+        const uint32_t nb = wbase(bn);
         // one block: wait until only the blocks issued after it are in flight
         // (DEPTH-1 weight loads, plus at most the next tile's scale DMAs,
         // which are younger), compute it, refill its slot with the block
@@ -874,6 +880,7 @@ hipError_t by_shape(uint32_t G, const void* X, const void* W, const void* S, con
     if constexpr (MODE == Q8X) {
         const uint32_t nbpt = K / 64u;
         const bool lmh_ok = e_lmh && M > 8 && N >= 32768 && (G == 64 || G == 128) &&
+                            (uint64_t)N * K < 0x7FFF0000u &&
                             nbpt >= 16 && (nbpt & (nbpt - 1u)) == 0 &&
                             lmh_lds_bytes(M > 16 ? 2 : 1, K, G, 8) <= 160u * 1024u &&
                             ((uintptr_t)X & 15) == 0 && e_nt < 0 && e_nw < 0;
