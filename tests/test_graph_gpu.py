@@ -34,7 +34,8 @@ def _case(name, dev):
         y = torch.empty((M, 2048), dtype=torch.bfloat16, device=dev)
         return (lambda: ops.gemv4_b(lin.q, lin.s, lin.b, x, y, 2048, 2048, M)), y
     if name.startswith("gemv8_b_vocab") or name.startswith("gemv4_b_vocab"):
-        # vocabulary-sized N: the four-wave skinny forms (8-bit M <= 8 stages x in LDS)
+        # vocabulary-sized N: the four-wave skinny forms (8-bit M <= 8 stages x
+        # in LDS) and, 8-bit M > 8, the persistent form
         bits = 8 if name.startswith("gemv8") else 4
         M = int(name.split("_m")[1])
         N, K = 32768, 2048
@@ -44,8 +45,8 @@ def _case(name, dev):
         f = ops.gemv8_b if bits == 8 else ops.gemv4_b
         return (lambda: f(lin.q, lin.s, lin.b, x, y, N, K, M)), y
     if name.startswith("gemm_bf16"):
-        M, N, K = {"gemm_bf16_splitk": (256, 2560, 2048), "gemm_bf16_256": (1472, 8192, 2048),
-                   "gemm_bf16_skinny": (24, 2048, 2048)}[name]
+        M, N, K = {"gemm_bf16_splitk": (256, 2560, 2048), "gemm_bf16_192": (1472, 8192, 2048),
+                   "gemm_bf16_256": (2048, 8192, 2048), "gemm_bf16_skinny": (24, 2048, 2048)}[name]
         _, A = acts(M, K, seed=17, dev=dev)
         B = (torch.randn(N, K, device=dev) * 0.05).to(torch.bfloat16)
         C = torch.empty((M, N), dtype=torch.float32, device=dev)
@@ -82,8 +83,8 @@ def _case(name, dev):
 
 
 CASES = ["gemv4", "gemv8", "gemv4_b_m4", "gemv4_b_m8", "gemv4_b_m32", "gemv8_b_vocab_m8",
-         "gemv4_b_vocab_m24", "gemm_bf16_splitk",
-         "gemm_bf16_256", "gemm_bf16_skinny", "gemm_q4", "gemm_naive", "rmsnorm_gemv4",
+         "gemv8_b_vocab_m32", "gemv4_b_vocab_m24", "gemm_bf16_splitk",
+         "gemm_bf16_192", "gemm_bf16_256", "gemm_bf16_skinny", "gemm_q4", "gemm_naive", "rmsnorm_gemv4",
          "silu_mul_gemv4", "dequant_tile"]
 
 
@@ -157,3 +158,52 @@ def test_graph_replay_after_workspace_growth(dev):
         g.replay()
         torch.cuda.synchronize()
         np.testing.assert_array_equal(ops.bits_of(y1), ref, err_msg=f"replay {r} after growth")
+
+
+_FIRST_CAPTURE = r"""
+import sys
+sys.path.insert(0, sys.argv[1])
+import numpy as np
+import torch
+from miori_amd import _lib, ops
+from tests.gpu_util import acts, weights
+_lib.load()
+dev = torch.device("cuda:0")
+M, N, K = 32, 32768, 2048
+_, lin = weights(N, K, 64, 8, seed=77, dev=dev)
+_, x = acts(M, K, seed=78, dev=dev)
+y = torch.zeros((M, N), dtype=torch.bfloat16, device=dev)
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):
+    ops.gemv8_b(lin.q, lin.s, lin.b, x, y, N, K, M)
+torch.cuda.synchronize()
+outs = []
+for r in range(2):
+    y.zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    outs.append(ops.bits_of(y).copy())
+y2 = torch.empty_like(y)
+ops.gemv8_b(lin.q, lin.s, lin.b, x, y2, N, K, M)
+torch.cuda.synchronize()
+ref = ops.bits_of(y2)
+for o in outs:
+    np.testing.assert_array_equal(o, ref)
+print("ok")
+"""
+
+
+def test_graph_capture_first_call_persistent(dev):
+    """The persistent 8-bit kernel's first call on a device may be made under
+    graph capture (it sets the kernel's dynamic-LDS limit once per device
+    then): in a fresh process the captured first call replays twice and
+    matches a later eager call bit for bit."""
+    import os
+    import subprocess
+    import sys
+
+    say("graph capture of the first persistent-kernel call (child process)")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", _FIRST_CAPTURE, root], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 0 and "ok" in r.stdout, r.stderr[-2000:]
