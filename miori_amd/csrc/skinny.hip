@@ -525,7 +525,7 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
     }
 }
 
-// Persistent 8-bit exact kernel for vocabulary-sized N and 9 <= M <= 32 (the
+// Persistent 8-bit exact kernel for vocabulary-sized N and 5 <= M <= 32 (the
 // batched lm_head): one workgroup of eight waves per CU stages x (M x K bf16)
 // in LDS once, and every wave then streams whole 16-row tiles of W over the
 // full K, tile w, w + W, w + 2W, ... of the grid's W waves. A wave keeps
@@ -542,7 +542,9 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
 //    wave per SIMD serialises its VALU and MFMA work), and so was the same
 //    loop with per-block address arithmetic instead of per-chunk bases with
 //    immediate offsets (73.2: 30% more VALU instructions).
-//    Up to M = 8 the skinny form with x in LDS stays the faster one.
+//    Up to M = 8 it replaced the four-wave form with x in LDS: M=8 65.8 ->
+//    60.5, M=6 62.4 -> 60.6, M=5 61.7 -> 60.1 (that form keeps the shapes
+//    this kernel does not take).
 //  * A tile's scales and biases (16 rows x K/G, contiguous) are DMA'd into a
 //    per-wave LDS double buffer just before the tile's first weight load,
 //    one 1 KiB chunk per instruction, so the wait for that block covers them;
@@ -875,11 +877,11 @@ hipError_t by_shape(uint32_t G, const void* X, const void* W, const void* S, con
     // which needs whole 512-element chunks of 16-byte aligned rows.
     const bool nw4_ok = sk == 1 && K / kb <= 32 &&
                         (MODE != Q8X || M > 8 || K > 2048 || (K % 512 == 0 && ((uintptr_t)X & 15) == 0));
-    // 8-bit, M > 8 at vocabulary-sized N: the persistent form with x in LDS
+    // 8-bit at vocabulary-sized N: the persistent form with x in LDS
     static const int e_lmh = tuning_env("MIORI_SKINNY_LMH", 1);
     if constexpr (MODE == Q8X) {
         const uint32_t nbpt = K / 64u;
-        const bool lmh_ok = e_lmh && M > 8 && N >= 32768 && (G == 64 || G == 128) &&
+        const bool lmh_ok = e_lmh && N >= 32768 && (G == 64 || G == 128) &&
                             (uint64_t)N * K < 0x7FFF0000u &&
                             nbpt >= 16 && (nbpt & (nbpt - 1u)) == 0 &&
                             lmh_lds_bytes(M > 16 ? 2 : 1, K, G, 8) <= 160u * 1024u &&

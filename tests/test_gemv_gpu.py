@@ -187,7 +187,8 @@ def test_batched_skinny_groups(dev, bits, M, N, K, G):
 
 @pytest.mark.parametrize("bits,M,N,K,G", [
     (4, 6, 32784, 1024, 32), (4, 20, 32768, 2048, 128), (4, 32, 40000, 4096, 64),
-    (8, 5, 32800, 1024, 128), (8, 12, 32768, 2048, 32), (8, 9, 33024, 512, 64),
+    (8, 5, 32800, 1024, 32), (8, 12, 32768, 2048, 32), (8, 9, 33024, 512, 64),
+    (8, 6, 33024, 2048, 32),
 ])
 def test_batched_skinny_four_wave(dev, bits, M, N, K, G):
     """Vocabulary-sized N: the four-wave workgroups (two n-tiles up to M = 8,
@@ -202,11 +203,12 @@ def test_batched_skinny_four_wave(dev, bits, M, N, K, G):
 
 
 @pytest.mark.parametrize("M,N,K,G", [
+    (5, 32776, 2048, 64), (8, 32768, 1024, 128),
     (9, 40008, 1024, 128), (16, 32768, 2048, 128), (12, 32768, 4096, 128),
     (17, 32784, 2048, 64), (32, 50000, 1024, 64),
 ])
 def test_gemv8_batched_persistent(dev, M, N, K, G):
-    """8-bit, 9 <= M <= 32 at vocabulary-sized N: the persistent form (x in
+    """8-bit, 5 <= M <= 32 at vocabulary-sized N: the persistent form (x in
     LDS once per CU, whole 16-row tiles over the full K per wave), with ragged
     N, one and two m-tiles, 16 to 64 blocks per tile and 16 or 32 of them in
     flight."""
