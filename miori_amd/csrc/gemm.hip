@@ -513,39 +513,24 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     store_wave_tile<CF>(acc, lds, wave, lane, wm, wn, m0, n0, M, N, C, out_bf16, part, ksp, SK);
 }
 
-// Producer / consumer form of the GEMM: eight waves, two per SIMD.
+// Producer / consumer form of the bf16 GEMM: eight waves, two per SIMD.
 // Waves 0-3 (consumers, 2x2 grid of (BM/2) x (BN/2) tiles) only read MFMA
 // fragments from LDS and run the MFMAs; waves 4-7 (producers) fill the
-// 3-stage LDS ring. A consumer never waits on vector memory, so while one
-// wave of a SIMD waits for its operands the other keeps the matrix core
-// busy. At the barrier of tile kt the consumers have read all of tile kt
-// (stage kt % 3 is free) and tiles kt+1 and kt+2 are complete in LDS; the
-// producers then fill the freed stage with tile kt+3.
-//  * A (both forms) and bf16 B: global -> LDS DMA, two tiles in flight
-//    behind the one being multiplied.
-//  * Fused 4-bit B (Q4): each producer thread owns one 32-code chunk of the
-//    128 x 64 tile (row t/2, half t%2). Its codes, scale and bias are loaded
-//    into registers one tile before they are needed (buffer loads: rows and
-//    groups past the operand read as zero and are never stored), then
-//    dequantised to bf16_rne(q*s + b) -- the dequant kernels' value -- and
-//    written to the swizzled bf16 B stage with ds_write_b128, while the
-//    consumers multiply. The matrix cores see exactly the operands of the
-//    two-step dequant + bf16 GEMM.
-// Per producer iteration (after the barrier of tile kt): issue A(kt+3) and
-// the codes of tile kt+4; wait for A(kt+2) and the codes of kt+3 (loads
-// complete in issue order); dequantise kt+3 into stage kt % 3; barrier. The
-// fragment order, MFMA sequence and epilogue are gemm_kernel's, so every
-// form gives bit-identical results.
-template <int BM, int BN, bool Q4, int G>
+// 3-stage LDS ring with A and B by global -> LDS DMA, two tiles in flight
+// behind the one being multiplied. A consumer never waits on vector memory,
+// so while one wave of a SIMD waits for its operands the other keeps the
+// matrix core busy. At the barrier of tile kt the consumers have read all of
+// tile kt (stage kt % 3 is free) and tiles kt+1 and kt+2 are complete in LDS;
+// the producers then fill the freed stage with tile kt+3. The fragment order,
+// MFMA sequence and epilogue are gemm_kernel's, so both forms give
+// bit-identical results.
+template <int BM, int BN>
 __global__ __launch_bounds__(512) void gemm_pc_kernel(
-    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B,
-    const uint32_t* __restrict__ q, const uint16_t* __restrict__ s,
-    const uint16_t* __restrict__ bsc, void* __restrict__ C, uint32_t M, uint32_t N,
-    uint32_t K, int out_bf16, uint32_t tiles_m, int remap, float* __restrict__ part,
-    uint32_t SK, uint32_t ntiles) {
-    using CF = Cfg<BM, BN, false, 64>;  // A / B ring and epilogue layout of the bf16 form
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
+    uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t tiles_m, int remap,
+    float* __restrict__ part, uint32_t SK, uint32_t ntiles) {
+    using CF = Cfg<BM, BN, false, 64>;
     static_assert(CF::NST == 3, "the producer / consumer ring has three stages");
-    static_assert(!Q4 || BN == 128, "fused: one producer thread per 32-code chunk of 128 rows");
     __shared__ __attribute__((aligned(1024))) uint8_t lds[CF::LDS];
 
     const uint32_t t = threadIdx.x;
@@ -568,9 +553,9 @@ __global__ __launch_bounds__(512) void gemm_pc_kernel(
 
     if (producer) {
         // DMA: producer wave w4 moves 8-row groups [w4*PA, (w4+1)*PA) of the A
-        // tile (and, bf16 B, [w4*PB, (w4+1)*PB) of the B tile); one
-        // instruction = 8 rows x 128 bytes, lane -> (row, swizzled chunk).
-        constexpr int PA = BM / 32, PB = Q4 ? 0 : BN / 32, PL = PA + PB;
+        // tile and [w4*PB, (w4+1)*PB) of the B tile; one instruction = 8 rows
+        // x 128 bytes, lane -> (row, swizzled chunk).
+        constexpr int PA = BM / 32, PB = BN / 32, PL = PA + PB;
         const uint32_t w4s = __builtin_amdgcn_readfirstlane(w4);
         uint32_t off[PL];
 #pragma unroll
@@ -592,144 +577,15 @@ __global__ __launch_bounds__(512) void gemm_pc_kernel(
                                                  : CF::B_OFF + st * CF::B_ST) + r0 * ROWB);
             }
         };
-        if constexpr (!Q4) {
-            issue(0, 0);
-            if (KT > 1) issue(1, 1);
-            if (KT > 2) issue(2, 2);
-            if (KT > 2) wait_vm<2 * PL>(); else if (KT > 1) wait_vm<PL>(); else wait_vm<0>();
-            barrier_lds();  // tile 0 has landed
-            for (uint32_t kt = 0; kt + 1 < KT; ++kt) {
-                if (kt + 2 < KT) wait_vm<PL>(); else wait_vm<0>();
-                barrier_lds();  // tile kt+1 has landed; stage kt % 3 is free
-                if (kt + 3 < KT) issue(kt + 3, kt % 3);
-            }
-        } else {
-            // This thread's chunk: row r of the tile, codes [32c, 32c + 32) of
-            // each 64-wide K tile.
-            const uint32_t pt = w4 * 64u + lane;
-            const uint32_t r = pt >> 1, c = pt & 1u;
-            const uint32_t row = n0 + r;  // rows >= N read zeros (never stored)
-            const uint32_t ng = K / G;
-            const rsrc_t rq = make_rsrc(q, N * (K / 2u));
-            const rsrc_t rs = make_rsrc(s, N * ng * 2u);
-            const rsrc_t rb = make_rsrc(bsc, N * ng * 2u);
-            const uint32_t qrow = row < N ? row * (K / 2u) + c * 16u : kOOB;
-            const uint32_t srow = row < N ? row * ng * 2u : kOOB;
-            struct Codes {
-                u32x4_t raw;
-                uint32_t sc, bi;
-            };
-            // The loads are inline asm, invisible to the compiler's own vmcnt
-            // waits (which would otherwise drain every load before the first
-            // use of a register loaded two iterations earlier); they are
-            // waited for by hand, and tie() keeps every use below the wait.
-            auto fetch = [&](uint32_t kt, Codes& x) {
-                const uint32_t kg = (kt0 + kt) * BK + c * 32u;  // first code of the chunk
-                const uint32_t so = srow == kOOB ? kOOB : srow + (kg / G) * 2u;
-                asm_load16(x.raw, rq, qrow == kOOB ? kOOB : qrow + (kt0 + kt) * (BK / 2u));
-                asm_load_u16(x.sc, rs, so);
-                asm_load_u16(x.bi, rb, so);
-            };
-            auto settle = [](Codes& x) {
-                tie(x.raw);
-                tie(x.sc);
-                tie(x.bi);
-            };
-            // bf16_rne(q*s + b) of the 32 codes into B stage st, row r,
-            // 16-byte chunks 4c .. 4c+3 (swizzled like the DMA'd bf16 tiles)
-            auto dequant = [&](const Codes& x, uint32_t st) {
-                const float sc = bf16_bits_to_f32(x.sc), bi = bf16_bits_to_f32(x.bi);
-                uint8_t* dst = lds + CF::B_OFF + st * CF::B_ST;
-#pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    const uint32_t v = x.raw[w];
-                    uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
-                    // opaque to the compiler, so byte j converts with one
-                    // v_cvt_f32_ubyte<j> instead of a bit-field extract + convert
-                    tie(lo);
-                    tie(hi);
-                    u32x4_t o;
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const float f0 = fmaf((float)((lo >> (8 * j)) & 0xFFu), sc, bi);
-                        const float f1 = fmaf((float)((hi >> (8 * j)) & 0xFFu), sc, bi);
-                        bf16x2_t pr = {(__bf16)f0, (__bf16)f1};
-                        o[j] = __builtin_bit_cast(uint32_t, pr);
-                    }
-                    *reinterpret_cast<u32x4_t*>(dst + swz(r, c * 4u + w)) = o;
-                }
-            };
-            constexpr int PQ = 3;  // vector loads per fetch
-            // Issue order per iteration: codes(kt+5), then A(kt+3). The codes
-            // of a tile are dequantised two iterations after they were
-            // issued, right after the barrier, without waiting for the A
-            // tile issued in between; the wait for A(kt+2) follows.
-            // prologue: codes(0..4) and A(0..2) in the steady-state order
-            // (codes(j+5) before A(j+3)); dequantise tiles 0..2
-            auto cl = [&](uint32_t kt) { return kt < KT ? kt : KT - 1u; };  // clamped tile
-            Codes x0, x1, x2, x3, x4;
-            fetch(0, x0);
-            fetch(cl(1), x1);
-            fetch(cl(2), x2);
-            issue(0, 0);
-            fetch(cl(3), x3);
-            if (KT > 1) issue(1, 1);
-            fetch(cl(4), x4);
-            if (KT > 2) issue(2, 2);
-            wait_vm<0>();
-            settle(x0);
-            settle(x1);
-            settle(x2);
-            settle(x3);
-            settle(x4);
-            dequant(x0, 0);
-            if (KT > 1) dequant(x1, 1);
-            if (KT > 2) dequant(x2, 2);
-            barrier_lds();  // tiles 0..2 are in LDS
-            // Steady state, after the barrier of tile kt (stage kt % 3 free):
-            // cur = codes(kt+3), codes(kt+4) in flight, fx receives
-            // codes(kt+5). Three code sets rotate (step kt dequantises
-            // R[kt % 3] and refills R[(kt + 2) % 3], whose tile was
-            // dequantised a step earlier); the loop body has no branches, so
-            // no register is reused while a load is still filling it.
-            auto step = [&](uint32_t kt, Codes& cur, Codes& fx) {
-                wait_vm<PQ + PL>();  // codes(kt+3); codes(kt+4) and A(kt+2) may be in flight
-                settle(cur);
-                dequant(cur, kt % 3);
-                fetch(cl(kt + 5), fx);
-                issue(kt + 3, kt % 3);
-                wait_vm<PQ + PL>();  // A(kt+2) has landed
-            };
-            uint32_t kt = 0;
-            for (; kt + 5 < KT; kt += 3) {  // steps kt .. kt+2 all fetch a real tile
-                barrier_lds();
-                step(kt, x3, x2);
-                barrier_lds();
-                step(kt + 1, x4, x3);
-                barrier_lds();
-                step(kt + 2, x2, x4);
-            }
-            // Tail: no more fetches; x3 / x4 hold codes(kt+3) / codes(kt+4).
-            wait_vm<0>();
-            settle(x3);
-            settle(x4);
-            if (kt + 1 < KT) {
-                barrier_lds();
-                if (kt + 3 < KT) {
-                    dequant(x3, kt % 3);
-                    issue(kt + 3, kt % 3);
-                }
-                wait_vm<0>();
-            }
-            if (kt + 2 < KT) {
-                barrier_lds();
-                if (kt + 4 < KT) {
-                    dequant(x4, (kt + 1) % 3);
-                    issue(kt + 4, (kt + 1) % 3);
-                }
-                wait_vm<0>();
-            }
-            for (kt += 2; kt + 1 < KT; ++kt) barrier_lds();
+        issue(0, 0);
+        if (KT > 1) issue(1, 1);
+        if (KT > 2) issue(2, 2);
+        if (KT > 2) wait_vm<2 * PL>(); else if (KT > 1) wait_vm<PL>(); else wait_vm<0>();
+        barrier_lds();  // tile 0 has landed
+        for (uint32_t kt = 0; kt + 1 < KT; ++kt) {
+            if (kt + 2 < KT) wait_vm<PL>(); else wait_vm<0>();
+            barrier_lds();  // tile kt+1 has landed; stage kt % 3 is free
+            if (kt + 3 < KT) issue(kt + 3, kt % 3);
         }
     } else {
         __builtin_amdgcn_s_setprio(2);
@@ -794,6 +650,235 @@ __global__ __launch_bounds__(512) void gemm_pc_kernel(
         store_wave_tile<CF>(acc, lds, w4, lane, wm, wn, m0, n0, M, N, C, out_bf16, part, ksp, SK);
 }
 
+// Fused 4-bit GEMM with the weight operand straight to registers. Eight
+// waves as in gemm_pc_kernel: waves 4-7 only DMA the A tiles into the 3-stage
+// LDS ring; consumer wave w (0-3) owns the 32 columns n0 + 32w .. +31 of the
+// BM x 128 tile over all BM rows (BM/32 MFMA tiles of 32x32). It loads its
+// own 4-bit codes, scales and biases with buffer loads two K tiles ahead,
+// dequantises them in registers to the MFMA B fragment (bf16_rne(q*s + b),
+// the dequant kernels' value) between its MFMAs, and reads only A from LDS.
+//  * B never passes through LDS, and each code is dequantised once: one
+//    32-code word per lane per k-step feeds BM/32 MFMAs.
+//  * Fragment layout: in k-step ks lane half h = lane/32 holds k chunk
+//    4h + ks (the A fragments use the same order), so a lane's four k-steps
+//    are 32 consecutive codes of its row: one 16-byte load per K tile.
+//  * Rows past N load zeros (buffer loads out of range) and are never stored.
+// The MFMA operands and their order per output are those of gemm_kernel, so
+// results are bit-identical with the two-step dequant + bf16 GEMM.
+template <int BM>
+struct CfgQ {  // wave tile of the fused register-B form, for the epilogue
+    static constexpr int WM = BM, WN = 32, TM = BM / 32, TN = 1;
+    static constexpr int EPR = 128;  // 4 waves x 128 rows x 40 floats fit the A ring
+};
+
+template <int BM, int BN, int G>
+__global__ __launch_bounds__(512) void gemm_pcq_kernel(
+    const uint16_t* __restrict__ A, const uint32_t* __restrict__ q,
+    const uint16_t* __restrict__ s, const uint16_t* __restrict__ bsc, void* __restrict__ C,
+    uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t tiles_m, int remap,
+    float* __restrict__ part, uint32_t SK, uint32_t ntiles) {
+    using CF = Cfg<BM, BN, false, 64>;  // A ring layout of the bf16 form
+    using WQ = CfgQ<BM>;
+    static_assert(CF::NST == 3 && BN == 128, "three A stages, 128 columns = 4 waves x 32");
+    static_assert(4 * WQ::EPR * (WQ::WN + 8) * 4 <= CF::LDS && BM % WQ::EPR == 0, "epilogue fits");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[CF::LDS];
+
+    const uint32_t t = threadIdx.x;
+    const uint32_t lane = t & 63u, wave = t >> 6;
+    const bool producer = wave >= 4;
+    const uint32_t w4 = wave & 3u;
+
+    uint32_t pid = blockIdx.x;
+    const uint32_t nwg = gridDim.x;
+    if (remap && (nwg & 7u) == 0) pid = (pid & 7u) * (nwg >> 3) + (pid >> 3);
+    const uint32_t tile = pid % ntiles, ksp = pid / ntiles;
+    const uint32_t tm = tile % tiles_m, tn = tile / tiles_m;
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t KT_ALL = K / BK;
+    const uint32_t kt0 = KT_ALL * ksp / SK;
+    const uint32_t KT = KT_ALL * (ksp + 1) / SK - kt0;
+
+    f32x16_t acc[WQ::TM][1];
+
+    if (producer) {
+        // producer wave w4 moves 8-row groups [w4*PA, (w4+1)*PA) of the A tile
+        constexpr int PA = BM / 32;
+        const uint32_t w4s = __builtin_amdgcn_readfirstlane(w4);
+        uint32_t off[PA];
+#pragma unroll
+        for (int p = 0; p < PA; ++p) {
+            const uint32_t r = (w4 * PA + p) * 8u + (lane >> 3);
+            const uint32_t kb = (lane & 7u) ^ (r & 7u) ^ ((r >> 3) & 1u);
+            off[p] = min(m0 + r, M - 1u) * K * 2u + kb * 16u;
+        }
+        auto issue = [&](uint32_t kt, uint32_t st) {
+            const uint8_t* base = reinterpret_cast<const uint8_t*>(A) + (size_t)(kt0 + kt) * BK * 2u;
+#pragma unroll
+            for (int p = 0; p < PA; ++p)
+                dma16(base + off[p], lds + CF::A_OFF + st * CF::A_ST + (w4s * PA + p) * 8u * ROWB);
+        };
+        issue(0, 0);
+        if (KT > 1) issue(1, 1);
+        if (KT > 2) issue(2, 2);
+        if (KT > 2) wait_vm<2 * PA>(); else if (KT > 1) wait_vm<PA>(); else wait_vm<0>();
+        barrier_lds();  // tile 0 has landed
+        for (uint32_t kt = 0; kt + 1 < KT; ++kt) {
+            if (kt + 2 < KT) wait_vm<PA>(); else wait_vm<0>();
+            barrier_lds();  // tile kt+1 has landed; stage kt % 3 is free
+            if (kt + 3 < KT) issue(kt + 3, kt % 3);
+        }
+    } else {
+        __builtin_amdgcn_s_setprio(2);
+#pragma unroll
+        for (int i = 0; i < WQ::TM; ++i)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][0][e] = 0.f;
+
+        // this lane's weight row and k half
+        const uint32_t h = lane >> 5;
+        const uint32_t ng = K / G;
+        const rsrc_t rq = make_rsrc(q, N * (K / 2u));
+        const rsrc_t rs = make_rsrc(s, N * ng * 2u);
+        const rsrc_t rb = make_rsrc(bsc, N * ng * 2u);
+        const uint32_t n = n0 + w4 * 32u + (lane & 31u);
+        const uint32_t qoff = n < N ? n * (K / 2u) + h * 16u : kOOB;
+        const uint32_t soff = n < N ? n * ng * 2u : kOOB;
+        struct Codes {
+            u32x4_t raw;
+            uint32_t sc, bi;
+        };
+        constexpr int PQ = 3;  // vector loads per fetch
+        auto fetch = [&](uint32_t kt, Codes& x) {
+            const uint32_t kg = (kt0 + kt) * BK + h * 32u;  // first code of the lane's half
+            asm_load16(x.raw, rq, qoff == kOOB ? kOOB : qoff + (kt0 + kt) * (BK / 2u));
+            const uint32_t so = soff == kOOB ? kOOB : soff + (kg / G) * 2u;
+            asm_load_u16(x.sc, rs, so);
+            asm_load_u16(x.bi, rb, so);
+        };
+        auto settle = [](Codes& x) {
+            tie(x.raw);
+            tie(x.sc);
+            tie(x.bi);
+        };
+        // B fragment of k-step ks from word ks of the codes: elements 2i, 2i+1
+        // are nibbles 2i, 2i+1 of the word
+        auto deq = [](uint32_t v, float sc, float bi) {
+            uint32_t lo = v & 0x0F0F0F0Fu, hi = (v >> 4) & 0x0F0F0F0Fu;
+            tie(lo);
+            tie(hi);
+            u32x4_t o;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float f0 = fmaf((float)((lo >> (8 * i)) & 0xFFu), sc, bi);
+                const float f1 = fmaf((float)((hi >> (8 * i)) & 0xFFu), sc, bi);
+                bf16x2_t pr = {(__bf16)f0, (__bf16)f1};
+                o[i] = __builtin_bit_cast(uint32_t, pr);
+            }
+            return __builtin_bit_cast(bf16x8_t, o);
+        };
+
+        bf16x8_t af[2][WQ::TM], bq[2];
+        float fsc = 0.f, fbi = 0.f;
+        const uint32_t fsw = (lane & 7u) ^ ((lane >> 3) & 1u);
+        const uint32_t c0 = (4u * h) ^ fsw;
+        const uint32_t lrow = (lane & 31u) * ROWB;
+        auto read_a = [&](uint32_t kt, int ks, int slot) {
+            const uint32_t chunk = ((c0 ^ (uint32_t)ks) << 4) + lrow;
+            const uint32_t a_addr = CF::A_OFF + (kt % 3u) * CF::A_ST + chunk;
+#pragma unroll
+            for (int i = 0; i < WQ::TM; ++i)
+                asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(af[slot][i]) : "v"(a_addr), "i"(i * 32 * ROWB));
+        };
+        auto scales = [&](const Codes& x) {
+            fsc = bf16_bits_to_f32(x.sc);
+            fbi = bf16_bits_to_f32(x.bi);
+        };
+        auto make_b = [&](const Codes& x, int ks, int slot) { bq[slot] = deq(x.raw[ks], fsc, fbi); };
+        auto mfmas = [&](int slot) {
+#pragma unroll
+            for (int i = 0; i < WQ::TM; ++i)
+                acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][i], bq[slot], acc[i][0], 0, 0, 0);
+        };
+        // one MFMA, then up to three VALU instructions (the next k-step's B
+        // fragment), so the dequant issues while the matrix core is busy
+        auto interleave = [] {
+#pragma unroll
+            for (int m = 0; m < WQ::TM; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+            }
+        };
+        auto cl = [&](uint32_t kt) { return kt < KT ? kt : KT - 1u; };  // clamped tile
+        // Tile kt with cur = codes(kt) (settled; its k-step 0 fragment and
+        // scales already made), nxt = codes(kt+1) in flight, fx free: fetch
+        // codes(kt+2) into fx, run k-steps 0..2 while making the next
+        // k-step's B fragment, then (past the barrier that publishes A(kt+1))
+        // wait for codes(kt+1) and make tile kt+1's k-step 0 fragment while
+        // k-step 3 runs. (last: no tile follows, so no A fragments are read
+        // for one)
+        auto step = [&](uint32_t kt, Codes& cur, Codes& nxt, Codes& fx, auto last) {
+            fetch(cl(kt + 2), fx);
+#pragma unroll
+            for (int ks = 0; ks < BK / 16 - 1; ++ks) {
+                read_a(kt, ks + 1, (ks + 1) & 1);
+                asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(WQ::TM) : "memory");  // k-step ks has landed
+                __builtin_amdgcn_sched_barrier(0);
+                make_b(cur, ks + 1, (ks + 1) & 1);
+                mfmas(ks & 1);
+                interleave();
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (!decltype(last)::value && kt + 1 < KT) {
+                barrier_lds();  // completes the last k-step's reads; A(kt+1) has landed
+                read_a(kt + 1, 0, 0);
+            } else {
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            }
+            wait_vm<PQ>();  // codes(kt+1) have landed; codes(kt+2) may be in flight
+            settle(nxt);
+            __builtin_amdgcn_sched_barrier(0);
+            scales(nxt);
+            make_b(nxt, 0, 0);
+            mfmas((BK / 16 - 1) & 1);
+            interleave();
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        Codes x0, x1, x2;
+        fetch(0, x0);
+        fetch(cl(1), x1);
+        wait_vm<PQ>();
+        settle(x0);
+        scales(x0);
+        make_b(x0, 0, 0);
+        barrier_lds();  // A(0) has landed
+        read_a(0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t kt = 0;
+        using More = std::false_type;
+        for (; kt + 3 <= KT; kt += 3) {
+            step(kt, x0, x1, x2, More{});
+            step(kt + 1, x1, x2, x0, More{});
+            step(kt + 2, x2, x0, x1, More{});
+        }
+        if (kt < KT) {
+            step(kt, x0, x1, x2, More{});
+            if (kt + 1 < KT) step(kt + 1, x1, x2, x0, std::true_type{});
+        }
+        // every code set stays live until its last load has landed (the last
+        // fetches fill sets that are never read)
+        wait_vm<0>();
+        settle(x0);
+        settle(x1);
+        settle(x2);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_setprio(0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    if (!producer)
+        store_wave_tile<WQ>(acc, lds, w4, lane, 0u, w4, m0, n0, M, N, C, out_bf16, part, ksp, SK);
+}
+
 // out[i] = sum over k = 0..SK-1 of part[k][i], in that order; 8 outputs per
 // thread (M*N is a multiple of 16).
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part,
@@ -855,12 +940,18 @@ hipError_t launch_cfg(const void* A, const void* B, const void* q, const void* s
         const hipError_t e = scratch_get(st, (size_t)SK * M * N * 4, &part);
         if (e != hipSuccess) return e;
     }
+    // the eight-wave forms for 256x128 and 128x128 tiles (MIORI_GEMM_PC=0:
+    // the four-wave gemm_kernel, for comparisons)
     static const int pc = tuning_env("MIORI_GEMM_PC", 1);
-    if constexpr (Cfg<BM, BN, false, 64>::NST == 3 && BM * BN >= 128 * 128) {
-        if (pc)
-            hipLaunchKernelGGL((gemm_pc_kernel<BM, BN, Q4, G>), dim3(ntiles * SK), dim3(512), 0,
-                               st, (const uint16_t*)A, (const uint16_t*)B, (const uint32_t*)q,
-                               (const uint16_t*)s, (const uint16_t*)b, C, M, N, K, out_bf16,
+    if constexpr (Cfg<BM, BN, false, 64>::NST == 3 && BM * BN >= 128 * 128 && BN == 128) {
+        if (pc && Q4)
+            hipLaunchKernelGGL((gemm_pcq_kernel<BM, BN, G>), dim3(ntiles * SK), dim3(512), 0, st,
+                               (const uint16_t*)A, (const uint32_t*)q, (const uint16_t*)s,
+                               (const uint16_t*)b, C, M, N, K, out_bf16, tiles_m, remap, part, SK,
+                               ntiles);
+        else if (pc)
+            hipLaunchKernelGGL((gemm_pc_kernel<BM, BN>), dim3(ntiles * SK), dim3(512), 0, st,
+                               (const uint16_t*)A, (const uint16_t*)B, C, M, N, K, out_bf16,
                                tiles_m, remap, part, SK, ntiles);
         else
             hipLaunchKernelGGL((gemm_kernel<BM, BN, Q4, G>), dim3(ntiles * SK), dim3(256), 0, st,

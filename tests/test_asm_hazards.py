@@ -76,13 +76,19 @@ def test_gemm_kernel_waits(tmp_path):
     bad = {k: v for k, v in res.items() if v}
     assert not bad, {k[:80]: v[:3] for k, v in bad.items()}
     assert not _spilled(text, "gemm_kernel")
-    # the producer / consumer form (bf16 and fused 4-bit; inline-asm code
-    # loads in the fused producers)
+    # the producer / consumer forms: bf16 (DMA producers) and fused 4-bit
+    # (consumers load their codes with inline-asm buffer loads two tiles
+    # ahead)
     res = check_file(text, "gemm_pc_kernel")
-    assert len(res) == 8, "expected every gemm_pc_kernel instantiation"
+    assert len(res) == 2, "expected every gemm_pc_kernel instantiation"
     bad = {k: v for k, v in res.items() if v}
     assert not bad, {k[:80]: v[:3] for k, v in bad.items()}
     assert not _spilled(text, "gemm_pc_kernel")
+    res = check_file(text, "gemm_pcq_kernel")
+    assert len(res) == 6, "expected every gemm_pcq_kernel instantiation"
+    bad = {k: v for k, v in res.items() if v}
+    assert not bad, {k[:80]: v[:3] for k, v in bad.items()}
+    assert not _spilled(text, "gemm_pcq_kernel")
 
 
 @pytest.mark.skipif(not shutil.which(HIPCC) and not os.path.exists(HIPCC), reason="hipcc not available")

@@ -83,6 +83,7 @@ def test_gemm_bf16_parity(dev, M, K, N):
     (1024, 2048, 8192, 64), (1472, 8192, 2048, 64), (256, 2048, 2560, 64),
     (1472, 2048, 8192, 64), (1500, 2048, 8208, 64),   # bf16 side on 192x256 / 256x256 tiles
     (1400, 2048, 8000, 64),
+    (1024, 2048, 2560, 64), (1000, 2048, 2608, 32), (1024, 2048, 8192, 128),  # 128x128 / G
     (32, 2048, 2048, 64), (32, 8192, 2048, 64), (100, 256, 48, 32), (64, 512, 128, 128),
     (32, 2048, 8192, 64), (9, 1024, 80, 32), (20, 2048, 512, 128),      # skinny path
 ])
