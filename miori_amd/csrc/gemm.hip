@@ -1025,19 +1025,23 @@ hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* 
                        const void* b, void* C, uint32_t M, uint32_t N, uint32_t K,
                        uint32_t G, int out_bf16, hipStream_t st) {
     // Tile choice (MIORI_GEMM_TILE overrides: 0 = 256x128, 1 = 128x128,
-    // 2 = 256x256, 3 = 64x128, 4 = 64x64, 5 = 192x256):
+    // 2 = 256x256, 3 = 64x128, 4 = 64x64, 5 = 192x256, 6 = 128x128 split as
+    // the 64x128 grid):
     //  * bf16 weight cache: 256x256 tiles (128 flop per operand byte, against
     //    85 for 256x128) once they fill at least 3/4 of the 256 CUs in a
     //    round; the split-K cost model is not applied to them (SK = 1).
     //    192x256 replaces them when its grid needs fewer rounds at 3/4 the
     //    cost per round: M=1472, N=8192, K=2048 62.7 -> 56.5 us, K=8192
     //    220 -> 194 us.
-    //  * small grids (K <= 4096, at most 512 64x64 tiles): 64x64 tiles (bf16)
-    //    or 64x128 (fused 4-bit), 2-3 workgroups per CU. Both paths take the
-    //    K split the cost model picks for the 64x128 grid (usually none), so
-    //    fused and bf16 products stay bit-identical. Measured against
-    //    128x128 tiles with split partials: bf16 M=1024 N=2048 19.7 -> 15.0
-    //    us, M=256 N=8192 19.9 -> 15.3 us; fused M=1024 N=512 25.8 -> 16.7.
+    //  * small grids (K <= 4096, at most 512 64x64 tiles): bf16 64x64 tiles,
+    //    2-3 workgroups per CU; fused 4-bit 128x128 (gemm_pcq_kernel). Both
+    //    paths take the K split the cost model picks for the 64x128 grid
+    //    (usually none), so fused and bf16 products stay bit-identical.
+    //    Measured against 128x128 tiles with their own split partials: bf16
+    //    M=1024 N=2048 19.7 -> 15.0 us, M=256 N=8192 19.9 -> 15.3 us. The
+    //    fused path's 128x128 register-B tiles against the four-wave 64x128
+    //    form: M=256 N=8192 30.1 -> 24.8 us, M=1024 N=2048 29.9 -> 24.3,
+    //    M=512 N=3072 28.7 -> 23.6, M=1024 N=512 17.6 -> 16.8.
     //  * otherwise 256x128 or 128x128 tiles, whichever the split-K cost
     //    model rates cheaper (pick_tile_256x128). Against the earlier rule
     //    (256x128 only in whole waves of 256): fused M=1472 N=8192 K=2048
@@ -1051,14 +1055,15 @@ hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* 
         // 6 x 32 = 192 256x256 tiles that leave a quarter of the CUs idle
         const uint64_t t192 = (uint64_t)((M + 191) / 192) * ((N + 255) / 256);
         tile = (t192 + 255) / 256 * 3 < (huge + 255) / 256 * 4 ? 5 : 2;
-    } else if (K <= 4096 && t64 <= 512) tile = q ? 3 : 4;
+    } else if (K <= 4096 && t64 <= 512) tile = q ? 6 : 4;
     static const int e_tile = tuning_env("MIORI_GEMM_TILE", -1);
     if (e_tile >= 0) tile = e_tile;
     if (tile == 2 && !q) return launch_cfg<256, 256, false, 64>(A, B, q, s, b, C, M, N, K, out_bf16, 1, st);
     if (tile == 5 && !q) return launch_cfg<192, 256, false, 64>(A, B, q, s, b, C, M, N, K, out_bf16, 1, st);
     if (tile == 2 || tile == 5) tile = pick_tile_256x128(M, N, K);  // fused: no 256x256 variant
-    // (64x64 splits as the 64x128 grid, the fused path's tile)
-    const uint32_t tbm = tile == 0 ? 256 : (tile == 3 || tile == 4) ? 64 : 128;
+    // (64x64, and the fused path's 128x128 tiles on these small grids, split
+    // as the 64x128 grid)
+    const uint32_t tbm = tile == 0 ? 256 : (tile == 3 || tile == 4 || tile == 6) ? 64 : 128;
     const uint32_t tbn = 128;
     const uint32_t ntiles = ((M + tbm - 1) / tbm) * ((N + tbn - 1) / tbn);
     // partial traffic from the padded tile grid, so every M in one row-tile
