@@ -1,30 +1,35 @@
 // Prefill GEMM on bf16 MFMA for gfx950: C[M][N] = A[M][K] . B[N][K]^T with
 // fp32 accumulation, B either the bf16 weight cache (row-major [N][K]) or the
-// 4-bit MLX-affine weights dequantised to bf16 on the way into LDS.
+// 4-bit MLX-affine weights dequantised to bf16 on the fly.
 //
 // Replaces shaders/gemm_mpp.metal:36-73 (gemm_mpp / gemm_mpp32, Apple MPP
 // matmul2d on a tile-major bf16 cache) and, for the fused variant, the
 // two-step dequant_tile + gemm_mpp of src/engine.cpp:144-146, 508-518.
 //
-// Structure (BM x BN macro tile per 256-thread workgroup, K in steps of 64):
+// Three kernels share the fragment layout, the MFMA order and the epilogue,
+// so every form gives bit-identical results for one K split:
+//  * gemm_kernel: four waves, each loading (DMA) and multiplying; the 256x256
+//    and 192x256 bf16 tiles, the 64x64 bf16 small-grid tiles, and (tuning
+//    overrides only) the fused form with B dequantised into LDS.
+//  * gemm_pc_kernel: bf16, eight waves, four consumers that only read LDS and
+//    run MFMAs, four producers that DMA the operands (256x128, 128x128).
+//  * gemm_pcq_kernel: fused 4-bit, eight waves, producers DMA A, each
+//    consumer loads and dequantises its own strip of B in registers
+//    (256x128, 128x128).
+// Common structure (K in steps of 64):
 //  * Operand tiles move HBM/L2 -> LDS with global_load_lds_dwordx4 (gfx950
-//    direct-to-LDS DMA): no staging registers, and the loads of step k+2 are
-//    in flight while step k runs on the matrix cores (3-stage LDS ring, one
-//    workgroup barrier per step, vmcnt waits placed by hand).
+//    direct-to-LDS DMA): no staging registers, several K tiles in flight
+//    (LDS ring, one workgroup barrier per step, vmcnt waits placed by hand).
 //  * Rows in LDS are 128 bytes (64 bf16); the 16-byte chunk kb of row r sits
 //    at slot kb ^ (r & 7) ^ ((r >> 3) & 1), so the 32 rows of an MFMA
 //    fragment read hit distinct banks. The DMA writes lanes in order, so the
 //    swizzle is applied by choosing which global chunk each lane fetches.
-//  * Four waves in a 2x2 grid, each a (BM/2) x (BN/2) tile of
-//    v_mfma_f32_32x32x16_bf16 accumulators. In k-step s of a 64-wide K tile,
+//  * v_mfma_f32_32x32x16_bf16 accumulators; in k-step s of a 64-wide K tile,
 //    lane half h = lane/32 of a fragment holds chunk 4h + s (any k order is
 //    valid as long as A and B use the same one).
-//  * Fused 4-bit B: the raw codes (32 bytes per row per K tile) and the
-//    per-group scale/bias are DMA'd like A, one step ahead; every thread then
-//    dequantises one 32-code chunk (bf16_rne(q*s + b), the exact bf16 value
-//    the dequant kernels write) into a double-buffered bf16 B tile. The MFMA
-//    operands are therefore identical to the two-step path, and so are the
-//    results, bit for bit.
+//  * Fused 4-bit B is dequantised to bf16_rne(q*s + b), the exact bf16 value
+//    the dequant kernels write, so the MFMA operands and the results equal the
+//    two-step path's, bit for bit.
 //  * Workgroups are renumbered so each XCD (workgroup id mod 8) works on a
 //    contiguous block of output tiles and keeps its operand slabs in its own
 //    L2. The epilogue stages the fp32 tile through LDS so every lane stores
