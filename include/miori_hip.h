@@ -141,8 +141,8 @@ int miori_gemm_bf16(const void* A, const void* B, void* C, uint32_t M,
                     uint32_t N, uint32_t K, int out_dtype, miori_stream stream);
 
 /* Fused 4-bit GEMM: as miori_gemm_bf16 with B = bf16(dequant4(W)), the
- * dequantisation done while the weight tile is staged to LDS, so the bf16
- * cache is never materialised. Numerically identical in operands to
+ * dequantisation done inside the GEMM (M > 32: in registers, just before the
+ * MFMAs that use it), so the bf16 cache is never materialised. Numerically identical in operands to
  * miori_dequant_q4_tile followed by miori_gemm_bf16 (the reference's two-step
  * dequant_tile + gemm_mpp, src/engine.cpp:144-146, 508-518).
  * Requires K % 64 == 0, N % 16 == 0, group in {32, 64, 128}. */

@@ -119,8 +119,8 @@ void linear(Metal& m, MTL::ComputeCommandEncoder* e, const Weights& w, const Ten
             const Tensor& s, const Tensor& b, MTL::Buffer* A, MTL::Buffer* C, uint32_t N,
             uint32_t K, uint32_t B, MTL::Buffer* bf16_cache = nullptr, uint32_t cache_off = 0);
 
-// No reference counterpart: the fused 4-bit GEMM (dequantisation inside the
-// GEMM's LDS staging), replacing the reference's dequant_tile + gemm_mpp
+// No reference counterpart: the fused 4-bit GEMM (the weights dequantised
+// inside the GEMM, never written as bf16), replacing the reference's dequant_tile + gemm_mpp
 // pair (src/engine.cpp:144-146, 508-518) without the bf16 cache.
 void gemm_q4(Metal& m, MTL::ComputeCommandEncoder* e, MTL::Buffer* A, const Weights& w,
              const Tensor& q, const Tensor& s, const Tensor& b, MTL::Buffer* C,

@@ -154,8 +154,8 @@ gemm_mpp32 = gemm_mpp    # src/ops.h:207-209 (32-row tile variant of the same pr
 
 
 def gemm_q4(A, q, s, b, C, M, N, K, group=64, stream=None):
-    """Fused 4-bit GEMM: C = A . bf16(dequant4(W))^T with the dequant done in
-    the LDS staging (no reference kernel; replaces the reference's
+    """Fused 4-bit GEMM: C = A . bf16(dequant4(W))^T with the dequant done
+    inside the GEMM (no reference kernel; replaces the reference's
     dequant_tile + gemm_mpp pair, src/engine.cpp:144-146, 508-518)."""
     if K % group:
         raise MioriError("miori_gemm_q4", -2, "K must be a multiple of the group size")
