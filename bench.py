@@ -82,6 +82,8 @@ def _parse():
     p.add_argument("--case", default=None,
                    help="time one case only, KIND,M,N,K with KIND gemv4 | gemv8 | gemm_bf16 | "
                         "gemm_q4 (for profiling runs)")
+    p.add_argument("--clock", action="store_true",
+                   help="with --case gemm_*: also sample the shader clock during a replay")
     p.add_argument("--calib-copy", action="store_true",
                    help="also run a 256 MiB device copy (reference for the HBM byte counters)")
     return p.parse_args()
@@ -137,6 +139,58 @@ class Timer:
         torch.cuda.synchronize()
         del g
         return s0.elapsed_time(s1), "hip-graph, caches flushed (1 GiB) before the timed replay"
+
+
+MFMA_PEAK_CLOCK_GHZ = 2.4  # the clock the dense bf16 peak is quoted at
+
+
+def shader_clock(c, fn, steps):
+    """Shader clock (GHz) while `steps` launches of fn(i) replay as a graph:
+    miori_diag_clock_sample runs on a side stream beside the replay and
+    records (s_memtime cycles, wall-clock ticks) pairs every 0.5 us; the clock
+    of each interval is d(cycles) / d(ticks) x the wall-clock rate. The
+    sampler holds one CU, so this replay is not the timed one."""
+    import ctypes
+    import numpy as np
+    from miori_amd import _lib
+    torch = c.torch
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    span_us = e0.elapsed_time(e1) * 1e3
+    gap = 50  # ticks of the 100 MHz wall clock
+    n = int(min(1 << 20, max(16, span_us * 100 / gap)))
+    buf = torch.zeros(2 * n, dtype=torch.int64, device=c.dev)
+    khz = ctypes.c_uint32(0)
+    side = torch.cuda.Stream(device=c.dev)
+    side.wait_stream(torch.cuda.current_stream())
+    _lib.call("miori_diag_clock_sample", ctypes.c_void_p(buf.data_ptr()), n, gap,
+              ctypes.byref(khz), ctypes.c_void_p(side.cuda_stream))
+    g.replay()
+    torch.cuda.synchronize()
+    del g
+    smp = buf.cpu().numpy().view(np.uint64).reshape(n, 2).astype(np.float64)
+    # single 0.5 us intervals are quantised by the wall clock's resolution:
+    # clocks are taken over 20-sample (10 us) windows and over the whole span
+    w = 20
+    dc = smp[w:, 0] - smp[:-w, 0]
+    dr = smp[w:, 1] - smp[:-w, 1]
+    ghz = dc[::w] / dr[::w] * khz.value * 1e3 / 1e9
+    mean = (smp[-1, 0] - smp[0, 0]) / (smp[-1, 1] - smp[0, 1]) * khz.value * 1e3 / 1e9
+    return {"mean_GHz": round(float(mean), 3), "median_GHz": round(float(np.median(ghz)), 3),
+            "p10_GHz": round(float(np.percentile(ghz, 10)), 3),
+            "p90_GHz": round(float(np.percentile(ghz, 90)), 3),
+            "windows": int(ghz.size), "window_us": round(w * gap * 1e3 / khz.value, 1),
+            "span_us": round(span_us, 1), "wall_clock_kHz": khz.value}
 
 
 def _rotating(t, copies):
@@ -212,7 +266,7 @@ def gemv_row(c, bits, M, N, K, G=64, steps=None, hot=False, tag=None):
     return row
 
 
-def gemm_row(c, M, N, K, fused, steps=30, vendor=False, G=64):
+def gemm_row(c, M, N, K, fused, steps=30, vendor=False, G=64, clock=False):
     """Config 3 (bf16 weight cache) or config 4 (fused 4-bit), bf16 out."""
     torch, ops = c.torch, c.ops
     q, s, b = _dev_quant(torch, c.dev, N, K, G, 4, c.gen)
@@ -245,10 +299,19 @@ def gemm_row(c, M, N, K, fused, steps=30, vendor=False, G=64):
                GB_s=round(nbytes / (us * 1e-6) / 1e9, 1), flops=flops, bytes=nbytes,
                roofline=roofline(us, nbytes, flops), steps=steps, copies=copies,
                copies_touched=min(steps, copies), bytes_touched=steps * wbytes, timing=mode)
+    if clock:
+        clk = shader_clock(c, fn, steps)
+        clk["mfma_peak_at_clock_TFLOP_s"] = round(
+            BF16_PEAK_TFLOPS * clk["mean_GHz"] / MFMA_PEAK_CLOCK_GHZ, 1)
+        clk["frac_at_clock"] = round(row["TFLOP_s"] / clk["mfma_peak_at_clock_TFLOP_s"], 4)
+        row["clock"] = clk
     if vendor and not fused:
-        vt, _ = c.timer.run(lambda i: torch.matmul(A, Bs[i % copies].t(), out=C), steps, 5)
+        vfn = lambda i: torch.matmul(A, Bs[i % copies].t(), out=C)  # noqa: E731
+        vt, _ = c.timer.run(vfn, steps, 5)
         row["hipblaslt_us"] = round(vt * 1e3 / steps, 2)
         row["hipblaslt_TFLOP_s"] = round(flops / (vt * 1e-3 / steps) / 1e12, 1)
+        if clock:
+            row["hipblaslt_clock"] = shader_clock(c, vfn, steps)
     torch.cuda.empty_cache()
     return row
 
@@ -518,7 +581,8 @@ def main():
         if kind in ("gemv4", "gemv8"):
             row = gemv_row(c, 4 if kind == "gemv4" else 8, M, N, K)
         elif kind in ("gemm_bf16", "gemm_q4"):
-            row = gemm_row(c, M, N, K, kind == "gemm_q4", steps=min(args.steps, 30))
+            row = gemm_row(c, M, N, K, kind == "gemm_q4", steps=min(args.steps, 30),
+                           vendor=args.clock and kind == "gemm_bf16", clock=args.clock)
         else:
             raise SystemExit(f"unknown case kind {kind}")
         if args.calib_copy:
@@ -532,7 +596,8 @@ def main():
             calib_copy(torch, dev)
         print(json.dumps({"gemv4": head, "gemv_floors": floors}), flush=True)
         return
-    gemm = log(gemm_row(c, 1024, 8192, 2048, False, steps=min(args.steps, 100), vendor=True))
+    gemm = log(gemm_row(c, 1024, 8192, 2048, False, steps=min(args.steps, 100), vendor=True,
+                        clock=True))
 
     rows = [dict(config=0, **head)]
     for K, N in [(2048, 8192), (2048, 2048), (2048, 512), (8192, 2048)]:
@@ -601,7 +666,8 @@ def main():
         "gemm": {"workload": "bf16 GEMM M=1024 K=2048 N=8192, bf16 out (config 3)",
                  "us": gemm["us"], "TFLOP_s": gemm["TFLOP_s"], "roofline": gemm["roofline"],
                  "hipblaslt_us": gemm["hipblaslt_us"],
-                 "hipblaslt_TFLOP_s": gemm["hipblaslt_TFLOP_s"]},
+                 "hipblaslt_TFLOP_s": gemm["hipblaslt_TFLOP_s"],
+                 "clock": gemm["clock"], "hipblaslt_clock": gemm["hipblaslt_clock"]},
         "gemv_floors": floors,
         "gemv_hot_cache_us": head["hot_cache_us"],
         "configs": rows,

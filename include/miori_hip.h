@@ -212,6 +212,20 @@ int miori_dequant_q8(const void* q, const void* scales, const void* biases,
                      void* out, uint32_t N, uint32_t K, uint32_t group,
                      miori_stream stream);
 
+/* ---- diagnostics ---------------------------------------------------------
+ * No counterpart in the reference. Launches one wave on `stream` that records
+ * n pairs (shader-clock cycles from s_memtime, wall-clock ticks from
+ * s_memrealtime) into samples[2n], one pair every gap_ticks wall-clock ticks,
+ * and writes the wall-clock rate in kHz to *wall_khz (host pointer, set
+ * before the launch returns). Run beside a kernel on another stream, the
+ * clock it ran at over an interval is d(cycles) / d(ticks) x wall_khz. The
+ * wave holds a few registers of one CU until it ends, so a concurrent kernel
+ * that fills every CU runs slower meanwhile: use the samples for clocks, not
+ * for timing. Bounds: n <= 2^20, n x gap_ticks <= 2 s of wall clock;
+ * samples 8-byte aligned device memory. */
+int miori_diag_clock_sample(uint64_t* samples, uint32_t n, uint32_t gap_ticks,
+                            uint32_t* wall_khz, miori_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -36,6 +36,7 @@ SIGNATURES = {
     "miori_dequant_q4_tile": ([_P, _P, _P, _P, _U, _U, _U, _P], _I),
     "miori_dequant_q4": ([_P, _P, _P, _P, _U, _U, _U, _P], _I),
     "miori_dequant_q8": ([_P, _P, _P, _P, _U, _U, _U, _P], _I),
+    "miori_diag_clock_sample": ([_P, _U, _U, _P, _P], _I),
 }
 
 _lib = None

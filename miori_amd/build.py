@@ -31,7 +31,7 @@ HOST_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__",
               f"-I{ROCM}/include"]
 HOST_LINK = [f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib"]
 
-SOURCES = ["gemv.hip", "skinny.hip", "dequant.hip", "gemm.hip", "naive.hip", "workspace.cpp",
+SOURCES = ["gemv.hip", "skinny.hip", "dequant.hip", "gemm.hip", "naive.hip", "diag.hip", "workspace.cpp",
            "capi.cpp", "noalloc.cpp"]
 
 FLAGS = [

@@ -15,6 +15,9 @@ using namespace miori;
 namespace {
 
 constexpr uint64_t kMaxBytes = 0xFFFFFFF0ull;
+// Clock sampler bounds: at most 2^20 samples and 2 s of wall clock (100 MHz).
+constexpr uint32_t kClockMaxSamples = 1u << 20;
+constexpr uint64_t kClockMaxTicks = 200000000ull;
 // miori_linear_q4 takes the exact 4-bit batched GEMV up to this many rows.
 constexpr uint32_t kLinearExactMaxM = 32;
 
@@ -244,6 +247,21 @@ int miori_dequant_q4(const void* q, const void* scales, const void* biases, void
 int miori_dequant_q8(const void* q, const void* scales, const void* biases, void* out,
                      uint32_t N, uint32_t K, uint32_t group, miori_stream stream) {
     return dequant_common(8, q, scales, biases, out, N, K, group, (hipStream_t)stream);
+}
+
+int miori_diag_clock_sample(uint64_t* samples, uint32_t n, uint32_t gap_ticks,
+                            uint32_t* wall_khz, miori_stream stream) {
+    if (!samples || !wall_khz) return MIORI_E_NULL;
+    if (n == 0 || gap_ticks == 0 || n > kClockMaxSamples ||
+        (uint64_t)n * gap_ticks > kClockMaxTicks)
+        return MIORI_E_SHAPE;
+    if (!aligned(samples, 8)) return MIORI_E_ALIGN;
+    int dev = 0, khz = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess)
+        return MIORI_E_HIP;
+    *wall_khz = (uint32_t)khz;
+    return hip_status(launch_clock_sampler(samples, n, gap_ticks, (hipStream_t)stream));
 }
 
 }  // extern "C"

@@ -29,6 +29,10 @@ hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* 
                        const void* b, void* C, uint32_t M, uint32_t N, uint32_t K,
                        uint32_t G, int out_bf16, hipStream_t st);
 
+// One-wave sampler of (shader clock, wall clock) pairs, `gap` wall-clock
+// ticks apart, into out[2n].
+hipError_t launch_clock_sampler(uint64_t* out, uint32_t n, uint32_t gap, hipStream_t st);
+
 // C (fp32, row stride ldc) = A . B^T for any shape, bf16 operands with row
 // strides lda / ldb; one sequential fp32 FMA chain over k per output.
 hipError_t launch_gemm_naive(const void* A, const void* B, float* C, uint32_t M, uint32_t N,

@@ -72,6 +72,18 @@ def test_batched_and_gemm_argument_checks():
     assert _lib.status("miori_dequant_q8", FAKE, FAKE, FAKE, 0, 64, 128, 64, None) == -1
 
 
+def test_clock_sampler_argument_checks():
+    khz = ctypes.c_uint32(0)
+    st = lambda *a: _lib.status("miori_diag_clock_sample", *a)  # noqa: E731
+    assert st(0, 16, 50, ctypes.byref(khz), None) == -1            # null samples
+    assert st(FAKE, 16, 50, None, None) == -1                      # null wall_khz
+    assert st(FAKE, 0, 50, ctypes.byref(khz), None) == -2          # n = 0
+    assert st(FAKE, 16, 0, ctypes.byref(khz), None) == -2          # gap = 0
+    assert st(FAKE, (1 << 20) + 1, 1, ctypes.byref(khz), None) == -2   # too many samples
+    assert st(FAKE, 1 << 20, 1000, ctypes.byref(khz), None) == -2  # more than 2 s
+    assert st(FAKE + 4, 16, 50, ctypes.byref(khz), None) == -3     # misaligned
+
+
 def test_ops_rejects_host_tensors():
     import torch
 
