@@ -66,28 +66,41 @@ struct Sk {
     static constexpr int WL = MODE == BF16 ? STEPS : 1;        // 16-byte weight loads per n-tile
     // k-steps folded together (one quantisation group inside the block)
     static constexpr int SPF = !EXACT ? STEPS : ((G < KB ? G : KB) / 32);
-    // x staged in LDS once per workgroup (8-bit, the four-wave two-n-tile
-    // form used up to M = 8, whole K <= 2048): x fragments are then LDS
-    // reads, which leaves the vector memory path to the weight stream. XR:
-    // LDS row stride in bf16 (16-byte pad between rows).
-    static constexpr bool XL = MODE == Q8X && NWV == 4 && MT == 1 && NT == 2 && NBW * NWV * KB <= 2048;
-    static constexpr int XR = NBW * NWV * KB + 8;
-    // registers (dwords) per block slot, to size the pipeline depth
-    static constexpr int REGS = NT * WL * 4 + (XL ? 0 : MT * STEPS * 4);
-    static constexpr int PD0 = 136 / REGS;
-    static constexpr int PD = PD0 < 2 ? 2 : (PD0 > 4 ? 4 : PD0);   // blocks in flight per wave
-    static constexpr int TOT = NT * MT * 4 * 64;                  // partial floats per wave
-    static constexpr int L = NT * WL + (XL ? 0 : MT * STEPS);     // loads per block
+    static constexpr int NB = 16 * NT;
     // scale / bias tiles of the workgroup's rows in LDS (all K/G groups of up
     // to NBW * NWV blocks), rounded up to whole 1 KiB DMA chunks
-    static constexpr int NB = 16 * NT;
     // (all K / G groups of a row: sized for the largest supported K, 8 blocks
     // per wave, so a workgroup of a K split indexes groups absolutely)
     static constexpr int NGMAX = EXACT || MODE == Q4F ? (8 * NWV * KB) / G : 0;
     // (+ room for the masked reads of padding blocks past a row's end)
     static constexpr int SB_BYTES = ((NB * NGMAX * 2 + NBW * KB / 16 + 1023) / 1024) * 1024;
+    static constexpr int TOT = NT * MT * 4 * 64;                  // partial floats per wave
     static constexpr int RED_BYTES = NWV * TOT * 4;
-    static constexpr int LDS = 2 * SB_BYTES > RED_BYTES ? 2 * SB_BYTES : RED_BYTES;
+    // x tile in LDS (XL): the workgroup's 16*MT rows of x over its whole K
+    // range, rows padded to whole 128-element (256-byte) lengths, loaded once
+    // by 1 KiB DMAs; the x fragments are then LDS reads and the vector memory
+    // path carries only the weight stream. Taken wherever the tile (at the
+    // largest K range of the form, KW) fits beside the scale / bias tiles;
+    // the cross-wave reduction then reuses the tile's memory.
+    static constexpr int KW = NBW * NWV * KB;
+    static constexpr int XT_MAX = ((16 * MT * ((KW + 127) / 128 * 128) * 2 + 1023) / 1024) * 1024;
+    // A 64-128 KiB tile leaves one workgroup per CU, which only pays where
+    // the grid is one round: the eight-wave two-m-tile forms (M > 16, whose
+    // n-tiles per workgroup keep config-sized grids at <= 256 workgroups),
+    // and the 8-bit four-wave one-m-tile form (M <= 8, a 33 KiB tile).
+    // Measured against x loads per block (us): M=32 N=8192 K=2048 10.20 ->
+    // 9.67, fused GEMM M=24 N=2048 6.22 -> 5.67; one m-tile at M=16, N=16384
+    // (512 workgroups) 11.1 -> 13.1, so those forms keep the loads.
+    static constexpr bool XL =
+        2 * SB_BYTES + (XT_MAX > RED_BYTES ? XT_MAX : RED_BYTES) <= 160 * 1024 &&
+        ((NWV == 8 && MT == 2) || (MODE == Q8X && NWV == 4 && MT == 1 && NT == 2));
+    // registers (dwords) per block slot, to size the pipeline depth
+    static constexpr int REGS = NT * WL * 4 + (XL ? 0 : MT * STEPS * 4);
+    static constexpr int PD0 = 136 / REGS;
+    static constexpr int PD = PD0 < 2 ? 2 : (PD0 > 4 ? 4 : PD0);   // blocks in flight per wave
+    static constexpr int L = NT * WL + (XL ? 0 : MT * STEPS);     // loads per block
+    // static LDS: the scale / bias tiles, and without XL the reduction buffer
+    static constexpr int LDS = (XL || 2 * SB_BYTES > RED_BYTES) ? 2 * SB_BYTES : RED_BYTES;
     static constexpr int DEPTH = PD < NBW ? PD : NBW;             // slots actually used
     static_assert((DEPTH - 1) * L < 64, "vmcnt range");
 };
@@ -227,7 +240,9 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
     using C = Sk<MODE, MT, NT, G, NBW, NWV>;
     // scale / bias tiles first, the cross-wave reduction buffer at the end
     __shared__ __attribute__((aligned(1024))) uint8_t lds[C::LDS];
-    float* red = reinterpret_cast<float*>(lds);
+    // x tile (C::XL), sized by the launch; the reduction buffer reuses it
+    extern __shared__ __attribute__((aligned(1024))) uint8_t xdyn[];
+    float* red = reinterpret_cast<float*>(C::XL ? xdyn : lds);
     // LDS-typed pointers (ds_read, not flat loads that would wait on vmcnt)
     typedef __attribute__((address_space(3))) const uint16_t* lds_u16;
     const lds_u16 s_lds = (lds_u16)(lds);
@@ -262,20 +277,33 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) xrow[mt] = X + (size_t)min(m0 + mt * 16u + j, M - 1u) * K;
 
-    // x tile in LDS (C::XL): rows m0 .. m1-1 (one K split, whole K), one 1 KiB
-    // DMA per (row, 512-k chunk), issued before the first block so that
-    // block's wait covers it. Lanes of rows past m1 read row m1-1: their
-    // outputs are not stored.
-    extern __shared__ __attribute__((aligned(16))) uint8_t xdyn[];
+    // x tile in LDS (C::XL): rows m0 .. m0+xrows-1 over the workgroup's K
+    // range [kbase, kbase + nloc*KB), row r at r * rsb bytes; 16-byte chunk
+    // ch of a row is stored at chunk ch ^ (r & 15), so the 16 rows a
+    // fragment read touches at one k fall on distinct banks. DMA u fills
+    // tile bytes [1024u, 1024u + 1024), each lane the chunk its slot holds
+    // (source row and chunk clamped into x; such slots are never read). The
+    // DMAs are issued before the first block so its wait covers them.
     typedef __attribute__((address_space(3))) const u32x4_t* lds_v4;
-    const uint32_t xrows = min(16u, m1 - m0);
-    const lds_v4 xl_row = (lds_v4)(xdyn + min(j, xrows - 1u) * (uint32_t)C::XR * 2u);
+    const uint32_t xrows = min(16u * MT, m1 - m0);
+    const uint32_t kbase = kb0 * C::KB;
+    const uint32_t rsb = ((nloc * C::KB + 127u) & ~127u) * 2u;
+    uint32_t xrb[MT], xsw[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const uint32_t row = min(mt * 16u + j, xrows - 1u);
+        xrb[mt] = row * rsb;
+        xsw[mt] = row & 15u;
+    }
     if constexpr (C::XL) {
-        const uint32_t nch = K / 512u;
-        for (uint32_t u = wave; u < xrows * nch; u += NWV) {
-            const uint32_t r = u / nch, ch = u % nch;
-            dma16(X + (size_t)(m0 + r) * K + ch * 512u + lane * 8u,
-                  xdyn + r * (uint32_t)C::XR * 2u + ch * 1024u);
+        const uint32_t nins = (xrows * rsb + 1023u) / 1024u;
+        const uint32_t nch = nloc * C::KB / 8u;
+        for (uint32_t u = wave; u < nins; u += NWV) {
+            const uint32_t p = u * 1024u + lane * 16u;
+            const uint32_t r = p / rsb;
+            const uint32_t rr = min(r, xrows - 1u);
+            const uint32_t ch = min(((p - r * rsb) >> 4) ^ (r & 15u), nch - 1u);
+            dma16(X + (size_t)(m0 + rr) * K + kbase + ch * 8u, xdyn + u * 1024u);
         }
     }
 
@@ -337,14 +365,16 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
         constexpr int sl = i % C::DEPTH;
         bf16x8_t xf[MT][C::STEPS];
         // (the block's k base inside the workgroup's range, for the LDS x tile)
-        const uint32_t kx = min(b0 + (uint32_t)i, nblk - 1u) * C::KB;
+        const uint32_t kx = (min(b0 + (uint32_t)i, kb0 + nloc - 1u) - kb0) * C::KB;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
             for (int r = 0; r < C::STEPS; ++r) {
                 u32x4_t d;
-                if constexpr (C::XL)
-                    d = xl_row[(kx + kmap<MODE, G>(c, r)) / 8u];
+                if constexpr (C::XL) {
+                    const uint32_t ch = (kx + kmap<MODE, G>(c, r)) / 8u;
+                    d = *(lds_v4)(xdyn + xrb[mt] + ((ch ^ xsw[mt]) << 4));
+                }
                 else
                     d = xr[sl][mt][r];
                 if constexpr (!C::EXACT) {
@@ -469,7 +499,7 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
                 for (int r = 0; r < C::STEPS; ++r) tie(xr[sl][mt][r]);
         }
         // scale/bias tiles (and the x tile) landed for all waves
-        if constexpr (i == 0 && MODE != BF16) barrier_lds();
+        if constexpr (i == 0 && (MODE != BF16 || C::XL)) barrier_lds();
         // keep each block's work (and its scale reads) inside its step
         __builtin_amdgcn_sched_barrier(0);
         compute(ic<i>{}, (uint32_t)i < nb);
@@ -771,9 +801,28 @@ hipError_t launch_sk(const void* X, const void* W, const void* S, const void* B,
     using C = Sk<MODE, MT, NT, G, NBW, NWV>;
     size_t xbytes = 0;
     if constexpr (C::XL) {
-        // whole 1 KiB x chunks per row, 16-byte aligned rows, no K split
-        if (SK != 1 || K % 512 != 0 || ((uintptr_t)X & 15) != 0) return hipErrorInvalidValue;
-        xbytes = (size_t)std::min(16u, (M + MZ - 1) / MZ) * C::XR * 2;
+        // 16-byte aligned rows (K % 8 == 0 and an aligned X, which the C ABI
+        // checks); the tile of the workgroup's rows, or the reduction buffer
+        if (((uintptr_t)X & 15) != 0 || K % 8 != 0) return hipErrorInvalidValue;
+        const size_t rows = std::min<uint32_t>(16u * MT, (M + MZ - 1) / MZ);
+        const size_t tile = (rows * (((K / SK) + 127u) / 128u * 128u) * 2 + 1023) / 1024 * 1024;
+        xbytes = std::max<size_t>(tile, C::RED_BYTES);
+        if (tile > (size_t)C::XT_MAX) return hipErrorInvalidValue;
+        if (xbytes > 64 * 1024) {
+            // (dynamic LDS above 64 KiB is opted into once per device)
+            static bool attr[64] = {false};
+            int dev = 0;
+            hipError_t e = hipGetDevice(&dev);
+            if (e != hipSuccess) return e;
+            if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+            if (!attr[dev]) {
+                e = hipFuncSetAttribute((const void*)skinny_kernel<MODE, MT, NT, G, NBW, NWV>,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize,
+                                        160 * 1024 - C::LDS);
+                if (e != hipSuccess) return e;
+                attr[dev] = true;
+            }
+        }
     }
     hipLaunchKernelGGL((skinny_kernel<MODE, MT, NT, G, NBW, NWV>), dim3(nwg, SK, MZ), dim3(NWV * 64),
                        xbytes, st, (const uint16_t*)X, (const uint8_t*)W, (const uint16_t*)S,
@@ -838,10 +887,12 @@ hipError_t by_shape(uint32_t G, const void* X, const void* W, const void* S, con
     // n-tiles per workgroup: x is loaded once per workgroup and reused by
     // each n-tile; two while that still gives >= 256 workgroups (more rows
     // per workgroup measured slower: fewer workgroups in flight)
-    // four for the 32-row products of N >= 16384, where x (M x K bf16, loaded
-    // once per workgroup) outweighs a 2-tile workgroup's weights
+    // four for the 32-row products of N > 8192, where x (M x K bf16, loaded
+    // once per workgroup) outweighs a 2-tile workgroup's weights and the
+    // x tile in LDS leaves one workgroup per CU (grids of <= 256 up to
+    // N = 16384; N=12288 M=32 14.8 -> 13.6 us, N=10240 M=24 13.3 -> 12.5)
     int nt = (N >= 8192) ? 2 : 1;
-    if (M > 16 && N >= 16384) nt = 4;
+    if (M > 16 && N > 8192) nt = 4;
     // K split over workgroups for K >= 8192 at M > 8: a workgroup then loads
     // a quarter of x (M x 8192 bf16 is 512 KB at M = 32, against 64 KB of
     // its weights), and the fp32 partials are added by a second kernel.
@@ -873,10 +924,7 @@ hipError_t by_shape(uint32_t G, const void* X, const void* W, const void* S, con
     // 8-bit M=32 140 -> 117 us, M=16 90 -> 85, M=8 80.5 -> 78.7; 4-bit at
     // N = 65536 M=32 45.5 -> 38.5 us, M=8 25.0 -> 24.5 (four n-tiles: 26.4).
     // Needs the whole K in 8 blocks per wave and no K split.
-    // Up to M = 8 at K <= 2048 the 8-bit four-wave form stages x in LDS,
-    // which needs whole 512-element chunks of 16-byte aligned rows.
-    const bool nw4_ok = sk == 1 && K / kb <= 32 &&
-                        (MODE != Q8X || M > 8 || K > 2048 || (K % 512 == 0 && ((uintptr_t)X & 15) == 0));
+    const bool nw4_ok = sk == 1 && K / kb <= 32;
     // 8-bit at vocabulary-sized N: the persistent form with x in LDS
     static const int e_lmh = tuning_env("MIORI_SKINNY_LMH", 1);
     if constexpr (MODE == Q8X) {

@@ -220,10 +220,30 @@ def test_gemv8_batched_persistent(dev, M, N, K, G):
     check_close(y, ref, f"gemv8_b persistent M={M} N={N} K={K}")
 
 
+@pytest.mark.parametrize("bits,M,N,K,G", [
+    (4, 9, 2048, 8704, 64),     # K split in 4: 2176 k per workgroup (17 x 128)
+    (8, 12, 1024, 8448, 32),    # K split in 4: 2112 k, rows padded to 2176 in LDS
+    (4, 32, 8192, 2048, 64),    # two m-tiles, the whole 2048 k in LDS (128 KiB)
+    (4, 32, 2048, 8192, 64),    # two m-tiles of a K split
+    (8, 7, 3000, 2560, 64),     # 2560 k: five 512-element pieces
+    (4, 13, 16400, 2048, 128),  # four n-tiles above M = 8 at N >= 16384
+])
+def test_batched_skinny_lds_x(dev, bits, M, N, K, G):
+    """The x tile in LDS over each workgroup's K range: K splits whose range
+    is no multiple of 512 (or of 128) elements, one and two m-tiles, against
+    the oracle."""
+    say(f"gemv{bits}_b LDS x M={M} N={N} K={K} G={G}")
+    w, lin = weights(N, K, G, bits, seed=M * 3 + K, dev=dev)
+    x, xd = acts(M, K, seed=M + 970, dev=dev)
+    y = _run(lin, xd, M, torch.bfloat16)
+    ref = oracle.gemv_f64(w.q, w.s, w.b, x, bits, K, G, nthreads=NT)
+    check_close(y, ref, f"gemv{bits}_b LDS x M={M} N={N} K={K}")
+
+
 def test_gemv8_batched_lds_x_fallback(dev):
-    """Up to M = 8 the 8-bit vocabulary-sized form stages x in LDS in whole
-    512-element chunks; K = 1280 takes the eight-wave form instead, with the
-    oracle's result. (A misaligned x is rejected by the entry point.)"""
+    """8-bit vocabulary-sized form at K = 1280 (x rows of two and a half
+    512-element pieces), with the oracle's result; a misaligned x is rejected
+    by the entry point."""
     M, N, K, G = 7, 32768, 1280, 32
     say(f"gemv8_b LDS-x fallback N={N} K={K} G={G}")
     w, lin = weights(N, K, G, 8, seed=K + G, dev=dev)
