@@ -27,6 +27,13 @@ def _case(name, dev):
         _, x = acts(1, 2048, seed=14, dev=dev)
         y = torch.empty(4096, dtype=torch.float32, device=dev)
         return (lambda: ops.gemv8(lin.q, lin.s, lin.b, x, y, 4096, 2048)), y
+    if name.startswith("gemv4_bk"):
+        # K = 8192 at M > 8: the K split folded in the kernel (counters)
+        M = int(name.split("_m")[1])
+        _, lin = weights(2048, 8192, 64, 4, seed=25 + M, dev=dev)
+        _, x = acts(M, 8192, seed=26 + M, dev=dev)
+        y = torch.empty((M, 2048), dtype=torch.bfloat16, device=dev)
+        return (lambda: ops.gemv4_b(lin.q, lin.s, lin.b, x, y, 2048, 8192, M)), y
     if name.startswith("gemv4_b"):
         M = int(name.split("_m")[1])
         _, lin = weights(2048, 2048, 64, 4, seed=15 + M, dev=dev)
@@ -82,7 +89,7 @@ def _case(name, dev):
     raise KeyError(name)
 
 
-CASES = ["gemv4", "gemv8", "gemv4_b_m4", "gemv4_b_m8", "gemv4_b_m32", "gemv8_b_vocab_m8",
+CASES = ["gemv4", "gemv8", "gemv4_b_m4", "gemv4_b_m8", "gemv4_b_m32", "gemv4_bk_m16", "gemv8_b_vocab_m8",
          "gemv8_b_vocab_m32", "gemv4_b_vocab_m24", "gemm_bf16_splitk",
          "gemm_bf16_192", "gemm_bf16_256", "gemm_bf16_skinny", "gemm_q4", "gemm_naive", "rmsnorm_gemv4",
          "silu_mul_gemv4", "dequant_tile"]
