@@ -6,8 +6,10 @@
 // matmul2d on a tile-major bf16 cache) and, for the fused variant, the
 // two-step dequant_tile + gemm_mpp of src/engine.cpp:144-146, 508-518.
 //
-// Three kernels share the fragment layout, the MFMA order and the epilogue,
-// so every form gives bit-identical results for one K split:
+// Three kernels share the LDS layout and the epilogue. gemm_kernel and
+// gemm_pcq_kernel run one MFMA sequence (32x32x16), so their results for one
+// K split are bit-identical; gemm_pc_kernel runs 16x16x32 MFMAs, whose
+// results differ from those by fp32 rounding of the k sums:
 //  * gemm_kernel: four waves, each loading (DMA) and multiplying; the 256x256
 //    and 192x256 bf16 tiles, the 64x64 bf16 small-grid tiles, and (tuning
 //    overrides only) the fused form with B dequantised into LDS.
@@ -24,12 +26,17 @@
 //    at slot kb ^ (r & 7) ^ ((r >> 3) & 1), so the 32 rows of an MFMA
 //    fragment read hit distinct banks. The DMA writes lanes in order, so the
 //    swizzle is applied by choosing which global chunk each lane fetches.
-//  * v_mfma_f32_32x32x16_bf16 accumulators; in k-step s of a 64-wide K tile,
-//    lane half h = lane/32 of a fragment holds chunk 4h + s (any k order is
-//    valid as long as A and B use the same one).
+//  * gemm_kernel / gemm_pcq_kernel: v_mfma_f32_32x32x16_bf16; in k-step s of
+//    a 64-wide K tile, lane half h = lane/32 of a fragment holds chunk 4h + s
+//    (any k order is valid as long as A and B use the same one).
+//    gemm_pc_kernel: v_mfma_f32_16x16x32_bf16, lane quarter q holds chunk
+//    2q + s in k-step s. Per flop the 16x16 MFMA reads and writes half the
+//    accumulator registers; under the board's power limit that energy is
+//    clock: 44 -> 38.7 us at M=1024, N=8192, K=2048.
 //  * Fused 4-bit B is dequantised to bf16_rne(q*s + b), the exact bf16 value
-//    the dequant kernels write, so the MFMA operands and the results equal the
-//    two-step path's, bit for bit.
+//    the dequant kernels write, so the MFMA operands equal the two-step
+//    path's, and so do the results wherever the two-step product runs on
+//    gemm_kernel (its 256x256, 192x256 and small-grid tiles).
 //  * Workgroups are renumbered so each XCD (workgroup id mod 8) works on a
 //    contiguous block of output tiles and keeps its operand slabs in its own
 //    L2. The epilogue stages the fp32 tile through LDS so every lane stores
@@ -106,11 +113,13 @@ struct Cfg {
 // bytes (fp32) per lane, or, split-K, the fp32 partial tile to part[ksp].
 // Only this wave touches its region, and a wave's LDS accesses complete in
 // order, so passes need no barrier.
-template <class CF>
-__device__ __forceinline__ void store_wave_tile(f32x16_t (&acc)[CF::TM][CF::TN], uint8_t* lds,
-                                                uint32_t wave, uint32_t lane, uint32_t wm,
-                                                uint32_t wn, uint32_t m0, uint32_t n0, uint32_t M,
-                                                uint32_t N, void* __restrict__ C, int out_bf16,
+// (stage(ep, ps) writes the pass-ps rows of the wave's accumulators to ep,
+// row stride CF::WN + 8 floats)
+template <class CF, class Stage>
+__device__ __forceinline__ void store_wave_rows(Stage&& stage, uint8_t* lds, uint32_t wave,
+                                                uint32_t lane, uint32_t wm, uint32_t wn,
+                                                uint32_t m0, uint32_t n0, uint32_t M, uint32_t N,
+                                                void* __restrict__ C, int out_bf16,
                                                 float* __restrict__ part, uint32_t ksp,
                                                 uint32_t SK) {
     constexpr uint32_t RS = CF::WN + 8;  // floats per LDS row
@@ -139,15 +148,7 @@ __device__ __forceinline__ void store_wave_tile(f32x16_t (&acc)[CF::TM][CF::TN],
     static_assert(CF::WM % EPR == 0 && EPR % 32 == 0, "passes cover whole 32-row MFMA tiles");
 #pragma unroll
     for (int ps = 0; ps < CF::WM / EPR; ++ps) {
-#pragma unroll
-        for (int i = ps * (EPR / 32); i < (ps + 1) * (EPR / 32); ++i)
-#pragma unroll
-            for (int j = 0; j < CF::TN; ++j)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const uint32_t r = (i - ps * (EPR / 32)) * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                    ep[r * RS + j * 32 + (lane & 31u)] = acc[i][j][e];
-                }
+        stage(ep, ps);
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const uint32_t rbase = m0 + wm * CF::WM + ps * EPR;  // first output row of this pass
         if (SK == 1) {
@@ -173,6 +174,61 @@ __device__ __forceinline__ void store_wave_tile(f32x16_t (&acc)[CF::TM][CF::TN],
         // the next pass rewrites this region: its reads must have returned
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
+}
+
+// 32x32 MFMA tiles: element e of lane l is row 8*(e/4) + 4*(l/32) + e%4,
+// column l%32 of its tile.
+template <class CF>
+__device__ __forceinline__ void store_wave_tile(f32x16_t (&acc)[CF::TM][CF::TN], uint8_t* lds,
+                                                uint32_t wave, uint32_t lane, uint32_t wm,
+                                                uint32_t wn, uint32_t m0, uint32_t n0, uint32_t M,
+                                                uint32_t N, void* __restrict__ C, int out_bf16,
+                                                float* __restrict__ part, uint32_t ksp,
+                                                uint32_t SK) {
+    constexpr uint32_t RS = CF::WN + 8;
+    constexpr int EPR = CF::EPR;
+    auto stage = [&](float* ep, int ps) {
+#pragma unroll
+        for (int i = 0; i < CF::TM; ++i) {
+            if (i < ps * (EPR / 32) || i >= (ps + 1) * (EPR / 32)) continue;
+#pragma unroll
+            for (int j = 0; j < CF::TN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const uint32_t r = (i - ps * (EPR / 32)) * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                    ep[r * RS + j * 32 + (lane & 31u)] = acc[i][j][e];
+                }
+        }
+    };
+    store_wave_rows<CF>(stage, lds, wave, lane, wm, wn, m0, n0, M, N, C, out_bf16, part, ksp, SK);
+}
+
+// 16x16 MFMA tiles (WM / 16 x WN / 16 of them): element e of lane l is row
+// 4*(l/16) + e, column l%16 of its tile.
+template <class CF>
+__device__ __forceinline__ void store_wave_tile16(f32x4_t (&acc)[CF::WM / 16][CF::WN / 16],
+                                                  uint8_t* lds, uint32_t wave, uint32_t lane,
+                                                  uint32_t wm, uint32_t wn, uint32_t m0,
+                                                  uint32_t n0, uint32_t M, uint32_t N,
+                                                  void* __restrict__ C, int out_bf16,
+                                                  float* __restrict__ part, uint32_t ksp,
+                                                  uint32_t SK) {
+    constexpr uint32_t RS = CF::WN + 8;
+    constexpr int EPR = CF::EPR;
+    auto stage = [&](float* ep, int ps) {
+#pragma unroll
+        for (int i = 0; i < CF::WM / 16; ++i) {
+            if (i < ps * (EPR / 16) || i >= (ps + 1) * (EPR / 16)) continue;
+#pragma unroll
+            for (int j = 0; j < CF::WN / 16; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t r = (i - ps * (EPR / 16)) * 16 + 4 * (lane >> 4) + e;
+                    ep[r * RS + j * 16 + (lane & 15u)] = acc[i][j][e];
+                }
+        }
+    };
+    store_wave_rows<CF>(stage, lds, wave, lane, wm, wn, m0, n0, M, N, C, out_bf16, part, ksp, SK);
 }
 
 template <int BM, int BN, bool Q4, int G>
@@ -526,9 +582,9 @@ __global__ __launch_bounds__(256) void gemm_kernel(
 // so while one wave of a SIMD waits for its operands the other keeps the
 // matrix core busy. At the barrier of tile kt the consumers have read all of
 // tile kt (stage kt % 3 is free) and tiles kt+1 and kt+2 are complete in LDS;
-// the producers then fill the freed stage with tile kt+3. The fragment order,
-// MFMA sequence and epilogue are gemm_kernel's, so both forms give
-// bit-identical results.
+// the producers then fill the freed stage with tile kt+3. The consumers run
+// 16x16x32 MFMAs (two k-steps per K tile); results differ from gemm_kernel's
+// 32x32x16 ones by fp32 rounding of the k sums.
 template <int BM, int BN>
 __global__ __launch_bounds__(512) void gemm_pc_kernel(
     const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
@@ -554,7 +610,8 @@ __global__ __launch_bounds__(512) void gemm_pc_kernel(
     const uint32_t kt0 = KT_ALL * ksp / SK;
     const uint32_t KT = KT_ALL * (ksp + 1) / SK - kt0;
 
-    f32x16_t acc[CF::TM][CF::TN];
+    constexpr int TM = CF::WM / 16, TN = CF::WN / 16;  // 16x16 MFMA tiles per wave
+    f32x4_t acc[TM][TN];
 
     if (producer) {
         // DMA: producer wave w4 moves 8-row groups [w4*PA, (w4+1)*PA) of the A
@@ -595,55 +652,58 @@ __global__ __launch_bounds__(512) void gemm_pc_kernel(
     } else {
         __builtin_amdgcn_s_setprio(2);
 #pragma unroll
-        for (int i = 0; i < CF::TM; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-            for (int j = 0; j < CF::TN; ++j)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
-        bf16x8_t af[2][CF::TM], bf[2][CF::TN];
+            for (int j = 0; j < TN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        // 16x16x32 MFMAs, two 32-deep k-steps per K tile. A fragment is 16
+        // rows (lane % 16) x 8 k; lane group q = lane / 16 supplies 16-byte
+        // chunk 2q + ks of the row in k-step ks, so over a K tile each lane
+        // reads the 32 contiguous bytes of k 16q .. 16q+15 (the B operand
+        // uses the same map, which is all an MFMA's k sum needs). A fragment
+        // row r = (multiple of 16) + lane % 16, so its swizzle term is
+        // f = (lane & 7) ^ ((lane >> 3) & 1) for every fragment.
+        bf16x8_t af[2][TM], bf[2][TN];
         const uint32_t fsw = (lane & 7u) ^ ((lane >> 3) & 1u);
-        const uint32_t c0 = (4u * (lane >> 5)) ^ fsw;
-        const uint32_t lrow = (lane & 31u) * ROWB;
+        const uint32_t c0 = (2u * (lane >> 4)) ^ fsw;
+        const uint32_t lrow = (lane & 15u) * ROWB;
         auto read_frags = [&](uint32_t kt, int ks, int slot) {
             const uint32_t chunk = ((c0 ^ (uint32_t)ks) << 4) + lrow;
             const uint32_t a_addr = CF::A_OFF + (kt % 3u) * CF::A_ST + wm * CF::WM * ROWB + chunk;
             const uint32_t b_addr = CF::B_OFF + (kt % 3u) * CF::B_ST + wn * CF::WN * ROWB + chunk;
 #pragma unroll
-            for (int i = 0; i < CF::TM; ++i)
-                asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(af[slot][i]) : "v"(a_addr), "i"(i * 32 * ROWB));
+            for (int i = 0; i < TM; ++i)
+                asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(af[slot][i]) : "v"(a_addr), "i"(i * 16 * ROWB));
 #pragma unroll
-            for (int j = 0; j < CF::TN; ++j)
-                asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(bf[slot][j]) : "v"(b_addr), "i"(j * 32 * ROWB));
+            for (int j = 0; j < TN; ++j)
+                asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(bf[slot][j]) : "v"(b_addr), "i"(j * 16 * ROWB));
         };
-        constexpr int NFR = CF::TM + CF::TN;
+        constexpr int NFR = TM + TN;
+        static_assert(NFR <= 15, "one k-step's reads fit the lgkm counter");
         auto mfmas = [&](int slot) {
 #pragma unroll
-            for (int i = 0; i < CF::TM; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < CF::TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[slot][i], bf[slot][j],
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[slot][i], bf[slot][j],
                                                                         acc[i][j], 0, 0, 0);
         };
         barrier_lds();  // tile 0 has landed
         read_frags(0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
         for (uint32_t kt = 0; kt < KT; ++kt) {
-#pragma unroll
-            for (int ks = 0; ks < BK / 16 - 1; ++ks) {
-                read_frags(kt, ks + 1, (ks + 1) & 1);
-                asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(NFR) : "memory");  // k-step ks has landed
-                __builtin_amdgcn_sched_barrier(0);
-                mfmas(ks & 1);
-                __builtin_amdgcn_sched_barrier(0);
-            }
+            read_frags(kt, 1, 1);
+            asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(NFR) : "memory");  // k-step 0 has landed
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(0);
+            __builtin_amdgcn_sched_barrier(0);
             if (kt + 1 < KT) {
-                barrier_lds();  // completes the last k-step's reads; tile kt+1 has landed
+                barrier_lds();  // completes k-step 1's reads; tile kt+1 has landed
                 read_frags(kt + 1, 0, 0);
             } else {
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             }
             __builtin_amdgcn_sched_barrier(0);
-            mfmas((BK / 16 - 1) & 1);
+            mfmas(1);
             __builtin_amdgcn_sched_barrier(0);
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -652,7 +712,7 @@ __global__ __launch_bounds__(512) void gemm_pc_kernel(
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     if (!producer)
-        store_wave_tile<CF>(acc, lds, w4, lane, wm, wn, m0, n0, M, N, C, out_bf16, part, ksp, SK);
+        store_wave_tile16<CF>(acc, lds, w4, lane, wm, wn, m0, n0, M, N, C, out_bf16, part, ksp, SK);
 }
 
 // Fused 4-bit GEMM with the weight operand straight to registers. Eight
@@ -669,7 +729,8 @@ __global__ __launch_bounds__(512) void gemm_pc_kernel(
 //    are 32 consecutive codes of its row: one 16-byte load per K tile.
 //  * Rows past N load zeros (buffer loads out of range) and are never stored.
 // The MFMA operands and their order per output are those of gemm_kernel, so
-// results are bit-identical with the two-step dequant + bf16 GEMM.
+// results are bit-identical with the two-step dequant + bf16 GEMM wherever
+// that runs on gemm_kernel (256x256, 192x256 and small-grid tiles).
 template <int BM>
 struct CfgQ {  // wave tile of the fused register-B form, for the epilogue
     static constexpr int WM = BM, WN = 32, TM = BM / 32, TN = 1;

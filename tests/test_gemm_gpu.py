@@ -88,8 +88,11 @@ def test_gemm_bf16_parity(dev, M, K, N):
     (32, 2048, 8192, 64), (9, 1024, 80, 32), (20, 2048, 512, 128),      # skinny path
 ])
 def test_gemm_q4_fused_parity(dev, M, K, N, G):
-    """Fused dequant-in-LDS GEMM: against the oracle, and bit-identical to the
-    two-step dequant_tile + gemm_mpp on the same operands."""
+    """Fused 4-bit GEMM: against the oracle, and against the two-step
+    dequant_tile + gemm_mpp on the same operands. Both take the same B values
+    (bf16_rne(q*s + b)); where the bf16 product runs on the 16x16x32
+    producer/consumer kernel and the fused one on 32x32x16 MFMAs, the two
+    differ only by fp32 rounding of the k sums, else bit for bit."""
     say(f"gemm_q4 M={M} K={K} N={N} G={G}")
     w, Bbits, A = _operands(M, N, K, seed=M * 3 + N, dev=dev, G=G)
     lin = ops.QuantLinear(w, dev)
@@ -104,7 +107,18 @@ def test_gemm_q4_fused_parity(dev, M, K, N, G):
     rows = _rows_for(M)
     ref = oracle.gemm_bf16_f64(A, Bbits, rows, nthreads=NT)
     check_close(ops.bits_of(C)[rows], ref, f"gemm_q4 {M}x{K}x{N}", f32_tight=True)
-    np.testing.assert_array_equal(ops.bits_of(C), ops.bits_of(C2))
+    _agree(ops.bits_of(C), ops.bits_of(C2), f"gemm_q4 vs two-step {M}x{K}x{N}")
+
+
+def _agree(a, b, what):
+    """Two fp32 products of the same bf16 operands with different MFMA
+    shapes: equal up to fp32 rounding of the k sums (2e-5 of the largest
+    magnitude; the products' own error against fp64 is checked separately)."""
+    a = np.asarray(a, dtype=np.float32)
+    b = np.asarray(b, dtype=np.float32)
+    tol = 2e-5 * float(np.abs(b).max())
+    err = float(np.abs(a - b).max())
+    assert err <= tol, f"{what}: max |diff| {err:.3e} > {tol:.3e}"
 
 
 @pytest.mark.parametrize("m_small,m_big", [(23, 32), (40, 64)])
@@ -146,9 +160,9 @@ np.save(sys.argv[7], C.cpu().numpy())
 @pytest.mark.parametrize("M,K,N", [(1024, 2048, 8192), (1472, 2048, 2560), (300, 8192, 2048)])
 def test_gemm_producer_consumer_matches_classic(dev, tmp_path, M, K, N):
     """The eight-wave producer/consumer bf16 GEMM (the default for 256x128
-    and 128x128 tiles) is bit-identical to the four-wave form
-    (MIORI_GEMM_PC=0, run in a child process: the switch is read once per
-    process)."""
+    and 128x128 tiles, 16x16x32 MFMAs) agrees with the four-wave form on the
+    same tiles (MIORI_GEMM_PC=0, 32x32x16 MFMAs, run in a child process: the
+    switch is read once per process) up to fp32 rounding of the k sums."""
     import subprocess
     import sys
 
@@ -167,4 +181,4 @@ def test_gemm_producer_consumer_matches_classic(dev, tmp_path, M, K, N):
     r = subprocess.run([sys.executable, "-c", _CLASSIC, root, str(M), str(N), str(K), str(fa),
                         str(fb), str(fc)], env=env, capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr[-2000:]
-    np.testing.assert_array_equal(C.cpu().numpy().view(np.uint32), np.load(fc).view(np.uint32))
+    _agree(C.cpu().numpy(), np.load(fc), f"producer/consumer vs four-wave {M}x{K}x{N}")
