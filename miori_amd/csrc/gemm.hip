@@ -6,18 +6,22 @@
 // matmul2d on a tile-major bf16 cache) and, for the fused variant, the
 // two-step dequant_tile + gemm_mpp of src/engine.cpp:144-146, 508-518.
 //
-// Three kernels share the LDS layout and the epilogue. gemm_kernel and
+// Four kernels share the LDS layout and the epilogue. gemm_kernel and
 // gemm_pcq_kernel run one MFMA sequence (32x32x16), so their results for one
-// K split are bit-identical; gemm_pc_kernel runs 16x16x32 MFMAs, whose
-// results differ from those by fp32 rounding of the k sums:
-//  * gemm_kernel: four waves, each loading (DMA) and multiplying; the 256x256
-//    and 192x256 bf16 tiles, the 64x64 bf16 small-grid tiles, and (tuning
-//    overrides only) the fused form with B dequantised into LDS.
+// K split are bit-identical; gemm_pc_kernel and gemm_w8_kernel run 16x16x32
+// MFMAs (one order, bit-identical with each other), whose results differ
+// from those by fp32 rounding of the k sums:
+//  * gemm_kernel: four waves, each loading (DMA) and multiplying; the 64x64
+//    bf16 small-grid tiles, and (tuning overrides only) the 256x256 and
+//    192x256 bf16 tiles and the fused form with B dequantised into LDS.
 //  * gemm_pc_kernel: bf16, eight waves, four consumers that only read LDS and
 //    run MFMAs, four producers that DMA the operands (256x128, 128x128).
 //  * gemm_pcq_kernel: fused 4-bit, eight waves, producers DMA A, each
 //    consumer loads and dequantises its own strip of B in registers
 //    (256x128, 128x128).
+//  * gemm_w8_kernel: bf16, eight waves that each DMA and multiply, 16x16x32
+//    MFMAs with gemm_pc_kernel's order (bit-identical with it): the 256x256
+//    and 192x256 tiles.
 // Common structure (K in steps of 64):
 //  * Operand tiles move HBM/L2 -> LDS with global_load_lds_dwordx4 (gfx950
 //    direct-to-LDS DMA): no staging registers, several K tiles in flight
@@ -945,6 +949,155 @@ __global__ __launch_bounds__(512) void gemm_pcq_kernel(
         store_wave_tile<WQ>(acc, lds, w4, lane, 0u, w4, m0, n0, M, N, C, out_bf16, part, ksp, SK);
 }
 
+// Eight-wave bf16 GEMM for the tall 192x256 and 256x256 tiles: every wave
+// both moves operands and multiplies. The waves form a 2 x 4 grid of
+// (BM/2) x 64 tiles on 16x16x32 MFMAs, the fragment map and MFMA order of
+// gemm_pc_kernel (so results are bit-identical with it), with accumulators
+// small enough for two waves per SIMD: one wave of a SIMD multiplies while
+// the other waits for LDS or issues DMA. Operands go global -> LDS by DMA
+// through a 2-stage ring (A then B per stage, 112 or 128 KiB); each wave
+// issues its share of K tile kt+2 between the MFMAs of tile kt's last k-step,
+// right after the barrier that frees that stage. At most 15 fragment reads
+// are in flight: a k-step's B reads go first, then a wait for the previous
+// k-step's reads, then its A reads.
+template <int BM, int BN>
+struct CfgW8 {
+    static constexpr int WM = BM / 2, WN = BN / 4;  // wave tile
+    static constexpr int EPR = 32;                  // epilogue rows per pass
+    static constexpr int A_ST = BM * ROWB, B_ST = BN * ROWB, ST = A_ST + B_ST;
+    static constexpr int LDS = 2 * ST;
+    static constexpr int INS = (BM + BN) / 8;       // DMA instructions per K tile
+    static constexpr int PW = INS / 8;              // per wave
+};
+
+template <int BM, int BN>
+__global__ __launch_bounds__(512) void gemm_w8_kernel(
+    const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
+    uint32_t M, uint32_t N, uint32_t K, int out_bf16, uint32_t tiles_m, int remap,
+    float* __restrict__ part, uint32_t SK, uint32_t ntiles) {
+    using CF = CfgW8<BM, BN>;
+    constexpr int TM = CF::WM / 16, TN = CF::WN / 16, NFR = TM + TN, PW = CF::PW;
+    static_assert(CF::INS % 8 == 0 && NFR <= 15 && TN <= 15, "DMA split and lgkm range");
+    static_assert(8 * CF::EPR * (CF::WN + 8) * 4 <= CF::LDS, "epilogue fits");
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[CF::LDS];
+
+    const uint32_t t = threadIdx.x;
+    const uint32_t lane = t & 63u, wave = t >> 6;
+    const uint32_t wm = wave >> 2, wn = wave & 3u;
+
+    uint32_t pid = blockIdx.x;
+    const uint32_t nwg = gridDim.x;
+    if (remap && (nwg & 7u) == 0) pid = (pid & 7u) * (nwg >> 3) + (pid >> 3);
+    const uint32_t tile = pid % ntiles, ksp = pid / ntiles;
+    const uint32_t tm = tile % tiles_m, tn = tile / tiles_m;
+    const uint32_t m0 = tm * BM, n0 = tn * BN;
+    const uint32_t KT_ALL = K / BK;
+    const uint32_t kt0 = KT_ALL * ksp / SK;
+    const uint32_t KT = KT_ALL * (ksp + 1) / SK - kt0;
+
+    // DMA instruction g = wave * PW + p moves 8 rows (lane -> row, swizzled
+    // chunk) of A (g < BM/8) or of B; per-lane offsets computed once
+    const uint32_t wave_s = __builtin_amdgcn_readfirstlane(wave);
+    uint32_t off[PW];
+#pragma unroll
+    for (int p = 0; p < PW; ++p) {
+        const uint32_t g = wave * PW + p;
+        const bool is_a = g < (uint32_t)(BM / 8);
+        const uint32_t r = (is_a ? g : g - BM / 8) * 8u + (lane >> 3);
+        const uint32_t kb = (lane & 7u) ^ (r & 7u) ^ ((r >> 3) & 1u);
+        const uint32_t row = is_a ? min(m0 + r, M - 1u) : min(n0 + r, N - 1u);
+        off[p] = row * K * 2u + kb * 16u;
+    }
+    auto issue_one = [&](uint32_t kt, uint32_t st, int p) {
+        const uint32_t g = wave_s * PW + p;
+        const bool is_a = g < (uint32_t)(BM / 8);
+        const uint8_t* base =
+            reinterpret_cast<const uint8_t*>(is_a ? A : B) + (size_t)(kt0 + kt) * BK * 2u;
+        const uint32_t dst = st * CF::ST + (is_a ? g * 8u * ROWB : CF::A_ST + (g - BM / 8) * 8u * ROWB);
+        dma16(base + off[p], lds + dst);
+    };
+    auto issue = [&](uint32_t kt, uint32_t st) {
+#pragma unroll
+        for (int p = 0; p < PW; ++p) issue_one(kt, st, p);
+    };
+
+    f32x4_t acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    bf16x8_t af[2][TM], bf[2][TN];
+    const uint32_t fsw = (lane & 7u) ^ ((lane >> 3) & 1u);
+    const uint32_t c0 = (2u * (lane >> 4)) ^ fsw;
+    const uint32_t lrow = (lane & 15u) * ROWB;
+    // fragments of k-step ks of tile kt into slot: B reads, then (read_next)
+    // a wait until the other slot's NFR reads have landed, then A reads
+    auto frag_addr = [&](uint32_t kt, int ks, bool b) {
+        const uint32_t chunk = ((c0 ^ (uint32_t)ks) << 4) + lrow;
+        return (kt & 1u) * CF::ST + (b ? CF::A_ST + wn * CF::WN * ROWB : wm * CF::WM * ROWB) + chunk;
+    };
+    auto read_b = [&](uint32_t kt, int ks, int slot) {
+        const uint32_t b_addr = frag_addr(kt, ks, true);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+            asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(bf[slot][j]) : "v"(b_addr), "i"(j * 16 * ROWB));
+    };
+    auto read_a = [&](uint32_t kt, int ks, int slot) {
+        const uint32_t a_addr = frag_addr(kt, ks, false);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+            asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(af[slot][i]) : "v"(a_addr), "i"(i * 16 * ROWB));
+    };
+    auto read_first = [&](uint32_t kt, int ks, int slot) {  // nothing else in flight
+        read_b(kt, ks, slot);
+        read_a(kt, ks, slot);
+    };
+    auto read_next = [&](uint32_t kt, int ks, int slot) {
+        if constexpr (NFR + TN > 15) asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(15 - TN) : "memory");
+        read_b(kt, ks, slot);
+        asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(TN) : "memory");
+        read_a(kt, ks, slot);
+    };
+    auto mfmas_dma = [&](int slot, bool dma, uint32_t dkt, uint32_t dst) {
+        constexpr int NM = TM * TN;
+#pragma unroll
+        for (int q = 0; q < NM; ++q) {
+            const int i = q / TN, j = q % TN;
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[slot][i], bf[slot][j], acc[i][j], 0, 0, 0);
+#pragma unroll
+            for (int p = (q * PW) / NM; p < ((q + 1) * PW) / NM; ++p)
+                if (dma) issue_one(dkt, dst, p);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    issue(0, 0);
+    if (KT > 1) issue(1, 1);
+    if (KT > 1) wait_vm<PW>(); else wait_vm<0>();
+    barrier_lds();  // tile 0 has landed
+    read_first(0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    for (uint32_t kt = 0; kt < KT; ++kt) {
+        read_next(kt, 1, 1);  // k-step 0's reads have landed
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas_dma(0, false, 0u, 0u);
+        __builtin_amdgcn_sched_barrier(0);
+        if (kt + 1 < KT) {
+            wait_vm<0>();   // this wave's share of tile kt+1 has landed
+            barrier_lds();  // k-step 1's reads done everywhere; tile kt+1 visible; stage kt&1 free
+            read_first(kt + 1, 0, 0);
+        } else {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas_dma(1, kt + 2 < KT, kt + 2, kt & 1u);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    store_wave_tile16<CF>(acc, lds, wave, lane, wm, wn, m0, n0, M, N, C, out_bf16, part, ksp, SK);
+}
+
 // out[i] = sum over k = 0..SK-1 of part[k][i], in that order; 8 outputs per
 // thread (M*N is a multiple of 16).
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ part,
@@ -1039,6 +1192,18 @@ hipError_t launch_cfg(const void* A, const void* B, const void* q, const void* s
 }
 
 template <int BM, int BN>
+hipError_t launch_w8(const void* A, const void* B, void* C, uint32_t M, uint32_t N, uint32_t K,
+                     int out_bf16, hipStream_t st) {
+    const uint32_t tiles_m = (M + BM - 1) / BM;
+    const uint32_t ntiles = tiles_m * ((N + BN - 1) / BN);
+    static const int remap = tuning_env("MIORI_GEMM_REMAP", 1);
+    hipLaunchKernelGGL((gemm_w8_kernel<BM, BN>), dim3(ntiles), dim3(512), 0, st,
+                       (const uint16_t*)A, (const uint16_t*)B, C, M, N, K, out_bf16, tiles_m,
+                       remap, nullptr, 1u, ntiles);
+    return hipGetLastError();
+}
+
+template <int BM, int BN>
 hipError_t launch_tile(const void* A, const void* B, const void* q, const void* s, const void* b,
                        void* C, uint32_t M, uint32_t N, uint32_t K, uint32_t G, int out_bf16,
                        uint32_t SK, hipStream_t st) {
@@ -1124,6 +1289,10 @@ hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* 
     } else if (K <= 4096 && t64 <= 512) tile = q ? 6 : 4;
     static const int e_tile = tuning_env("MIORI_GEMM_TILE", -1);
     if (e_tile >= 0) tile = e_tile;
+    // (MIORI_GEMM_W8=0: the four-wave gemm_kernel for these tiles, for comparisons)
+    static const int e_w8 = tuning_env("MIORI_GEMM_W8", 1);
+    if (tile == 2 && !q && e_w8) return launch_w8<256, 256>(A, B, C, M, N, K, out_bf16, st);
+    if (tile == 5 && !q && e_w8) return launch_w8<192, 256>(A, B, C, M, N, K, out_bf16, st);
     if (tile == 2 && !q) return launch_cfg<256, 256, false, 64>(A, B, q, s, b, C, M, N, K, out_bf16, 1, st);
     if (tile == 5 && !q) return launch_cfg<192, 256, false, 64>(A, B, q, s, b, C, M, N, K, out_bf16, 1, st);
     if (tile == 2 || tile == 5) tile = pick_tile_256x128(M, N, K);  // fused: no 256x256 variant
