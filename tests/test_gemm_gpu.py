@@ -182,3 +182,32 @@ def test_gemm_producer_consumer_matches_classic(dev, tmp_path, M, K, N):
                         str(fb), str(fc)], env=env, capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stderr[-2000:]
     _agree(C.cpu().numpy(), np.load(fc), f"producer/consumer vs four-wave {M}x{K}x{N}")
+
+
+@pytest.mark.parametrize("M,K,N", [(1472, 2048, 8192), (1500, 2048, 8208), (2048, 2048, 8192)])
+def test_gemm_eight_wave_matches_producer_consumer(dev, tmp_path, M, K, N):
+    """The eight-wave tall-tile kernel (192x256 and 256x256 tiles, the
+    default at these shapes) runs the producer/consumer kernel's 16x16x32
+    MFMA order, so its products equal those of the 256x128 producer/consumer
+    tiles (MIORI_GEMM_TILE=0, run in a child process: the switch is read
+    once per process) bit for bit, ragged edges included."""
+    import subprocess
+    import sys
+
+    say(f"gemm eight-wave vs producer/consumer M={M} K={K} N={N}")
+    w, Bbits, A = _operands(M, N, K, seed=M + 7 * N, dev=dev)
+    Ad = ops.to_device_bits(A, dev)
+    Bd = ops.to_device_bits(Bbits, dev)
+    C = torch.empty((M, N), dtype=torch.float32, device=dev)
+    ops.gemm_mpp(Ad, Bd, C, M, N, K)
+    torch.cuda.synchronize()
+    fa, fb, fc = tmp_path / "a.npy", tmp_path / "b.npy", tmp_path / "c.npy"
+    np.save(fa, A.view(np.int16))
+    np.save(fb, Bbits.view(np.int16))
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, MIORI_GEMM_TILE="0", MIORI_GEMM_SPLIT="1")
+    r = subprocess.run([sys.executable, "-c", _CLASSIC, root, str(M), str(N), str(K), str(fa),
+                        str(fb), str(fc)], env=env, capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-2000:]
+    np.testing.assert_array_equal(C.cpu().numpy().view(np.uint32), np.load(fc).view(np.uint32))
+
