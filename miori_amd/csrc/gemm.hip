@@ -35,8 +35,8 @@
 //    (any k order is valid as long as A and B use the same one).
 //    gemm_pc_kernel: v_mfma_f32_16x16x32_bf16, lane quarter q holds chunk
 //    2q + s in k-step s. Per flop the 16x16 MFMA reads and writes half the
-//    accumulator registers; under the board's power limit that energy is
-//    clock: 44 -> 38.7 us at M=1024, N=8192, K=2048.
+//    accumulator registers: 42.5 -> 37.3-39.9 us at M=1024, N=8192, K=2048,
+//    with a shader clock ~3% higher over the replay and fewer cycles.
 //  * Fused 4-bit B is dequantised to bf16_rne(q*s + b), the exact bf16 value
 //    the dequant kernels write, so the MFMA operands equal the two-step
 //    path's, and so do the results wherever the two-step product runs on
