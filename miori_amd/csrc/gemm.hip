@@ -682,6 +682,13 @@ __global__ __launch_bounds__(512) void gemm_pc_kernel(
                 asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(bf[slot][j]) : "v"(b_addr), "i"(j * 16 * ROWB));
         };
         constexpr int NFR = TM + TN;
+        // One k-step's reads fit the lgkm counter's 15. At the top of each
+        // K tile the next k-step's 12 reads are issued while the current
+        // one's 12 may still be in flight (24). gemm_w8_kernel keeps at most
+        // 15 in flight and runs the same fragment map and MFMA order; the
+        // two give bit-identical products on the GPU
+        // (test_gemm_eight_wave_matches_producer_consumer), and both pass
+        // the fp64 oracle checks.
         static_assert(NFR <= 15, "one k-step's reads fit the lgkm counter");
         auto mfmas = [&](int slot) {
 #pragma unroll
