@@ -1,0 +1,151 @@
+"""Host emulation of the LDS address maps of the GEMM and skinny kernels (no
+GPU): every DMA'd 16-byte chunk lands in one slot of its stage, each slot is
+written once, every fragment read finds the k chunk the MFMA lane map asks
+for, reads stay inside their operand's region, and the 16 lanes that LDS
+serves together hit 16 distinct 16-byte bank groups. The formulas restate
+the index arithmetic of gemm_w8_kernel, gemm_pc_kernel (miori_amd/csrc/
+gemm.hip) and the skinny kernel's x tile (miori_amd/csrc/skinny.hip); a
+change to one of them that breaks a mapping fails here before any GPU run."""
+import pytest
+
+ROWB = 128  # bytes per LDS row of a bf16 K tile (64 elements)
+
+
+def _swz_chunk(r, c):
+    """Logical 16-byte chunk stored at physical chunk c of LDS row r."""
+    return c ^ (r & 7) ^ ((r >> 3) & 1)
+
+
+def _check_frag_reads(addr_of, rows_of, region, want_chunk):
+    """addr_of(lane) -> byte address; rows_of(lane) -> tile row; checks the
+    chunk read, the region bound and banks for one 64-lane read."""
+    lo, hi = region
+    for grp in range(4):
+        banks = set()
+        for lane in range(16 * grp, 16 * grp + 16):
+            a = addr_of(lane)
+            assert lo <= a and a + 16 <= hi, (lane, a, region)
+            r = rows_of(lane)
+            assert a - lo == r * ROWB + (a - lo) % ROWB
+            phys = ((a - lo) % ROWB) // 16
+            assert _swz_chunk(r, phys) == want_chunk(lane), (lane, r, phys)
+            banks.add((a // 16) % 16)
+        assert len(banks) == 16, f"bank groups {sorted(banks)}"
+
+
+def _check_dma(writes, size):
+    """writes: iterable of (slot byte address, row, logical chunk); every
+    16-byte slot of [0, size) written once, holding the chunk its swizzle
+    position says."""
+    seen = {}
+    for a, r, kb in writes:
+        assert 0 <= a < size and a % 16 == 0
+        assert a not in seen, f"slot {a} written twice"
+        seen[a] = (r, kb)
+    assert len(seen) == size // 16, "every slot of the stage is written"
+    for a, (r, kb) in seen.items():
+        assert _swz_chunk(r, (a % ROWB) // 16) == kb
+
+
+@pytest.mark.parametrize("BM,BN", [(192, 256), (256, 256)])
+def test_eight_wave_maps(BM, BN):
+    WM, WN = BM // 2, BN // 4
+    A_ST, B_ST = BM * ROWB, BN * ROWB
+    PW = (BM + BN) // 8 // 8
+    writes = []
+    for w in range(8):
+        for p in range(PW):
+            g = w * PW + p
+            is_a = g < BM // 8
+            base = g * 8 * ROWB if is_a else A_ST + (g - BM // 8) * 8 * ROWB
+            for lane in range(64):
+                r = (g if is_a else g - BM // 8) * 8 + (lane >> 3)
+                kb = (lane & 7) ^ (r & 7) ^ ((r >> 3) & 1)
+                writes.append((base + lane * 16, r + (0 if is_a else BM), kb))
+    # rows of B follow A's in one stage: row index counted over the stage
+    _check_dma(((a, a // ROWB, kb) for a, _, kb in writes), A_ST + B_ST)
+    for wave in range(8):
+        wm, wn = wave >> 2, wave & 3
+        for ks in range(2):
+            def c0(lane):
+                return (2 * (lane >> 4)) ^ ((lane & 7) ^ ((lane >> 3) & 1))
+            for i in range(WM // 16):
+                _check_frag_reads(
+                    lambda lane: wm * WM * ROWB + ((c0(lane) ^ ks) << 4) + (lane & 15) * ROWB + i * 16 * ROWB,
+                    lambda lane: wm * WM + 16 * i + (lane & 15), (0, A_ST),
+                    lambda lane: 2 * (lane >> 4) + ks)
+            for j in range(WN // 16):
+                _check_frag_reads(
+                    lambda lane: A_ST + wn * WN * ROWB + ((c0(lane) ^ ks) << 4) + (lane & 15) * ROWB + j * 16 * ROWB,
+                    lambda lane: wn * WN + 16 * j + (lane & 15), (A_ST, A_ST + B_ST),
+                    lambda lane: 2 * (lane >> 4) + ks)
+    # epilogue staging of 8 waves x 32 rows x (WN + 8) floats inside the ring
+    assert 8 * 32 * (WN + 8) * 4 <= 2 * (A_ST + B_ST)
+
+
+@pytest.mark.parametrize("BM,BN", [(256, 128), (128, 128)])
+def test_producer_consumer_maps(BM, BN):
+    WM, WN = BM // 2, BN // 2
+    A_ST, B_ST = BM * ROWB, BN * ROWB
+    PA, PB = BM // 32, BN // 32
+    for is_a, PX, ST in ((True, PA, A_ST), (False, PB, B_ST)):
+        writes = []
+        for w4 in range(4):
+            for p in range(PX):
+                r0 = (w4 * PX + p) * 8
+                for lane in range(64):
+                    r = r0 + (lane >> 3)
+                    kb = (lane & 7) ^ (r & 7) ^ ((r >> 3) & 1)
+                    writes.append((r0 * ROWB + lane * 16, r, kb))
+        _check_dma(writes, ST)
+    for w4 in range(4):
+        wm, wn = w4 >> 1, w4 & 1
+        for ks in range(2):
+            def c0(lane):
+                return (2 * (lane >> 4)) ^ ((lane & 7) ^ ((lane >> 3) & 1))
+            for i in range(WM // 16):
+                _check_frag_reads(
+                    lambda lane: wm * WM * ROWB + ((c0(lane) ^ ks) << 4) + (lane & 15) * ROWB + i * 16 * ROWB,
+                    lambda lane: wm * WM + 16 * i + (lane & 15), (0, A_ST),
+                    lambda lane: 2 * (lane >> 4) + ks)
+            for j in range(WN // 16):
+                _check_frag_reads(
+                    lambda lane: wn * WN * ROWB + ((c0(lane) ^ ks) << 4) + (lane & 15) * ROWB + j * 16 * ROWB,
+                    lambda lane: wn * WN + 16 * j + (lane & 15), (0, B_ST),
+                    lambda lane: 2 * (lane >> 4) + ks)
+
+
+@pytest.mark.parametrize("KB,nloc,xrows", [
+    (128, 16, 8), (128, 16, 32), (128, 17, 9), (64, 33, 12), (64, 32, 32), (128, 4, 5),
+    (64, 40, 7), (128, 64, 16),
+])
+def test_skinny_x_tile_map(KB, nloc, xrows):
+    """The x tile: row r at r * rsb bytes, chunk ch of row r at chunk
+    ch ^ (r & 15); DMA u fills bytes [1024u, 1024u + 1024), lane -> its slot's
+    source chunk (clamped into the row)."""
+    kw = nloc * KB                    # elements of the workgroup's K range
+    rsb = ((kw + 127) // 128) * 128 * 2
+    nch = kw // 8
+    nins = (xrows * rsb + 1023) // 1024
+    tile = nins * 1024
+    held = {}
+    for u in range(nins):
+        for lane in range(64):
+            p = u * 1024 + lane * 16
+            r = p // rsb
+            rr = min(r, xrows - 1)
+            ch = min(((p - r * rsb) >> 4) ^ (r & 15), nch - 1)
+            assert p + 16 <= tile
+            held[p] = (rr, ch, r)
+    # every valid (row, chunk) is read from the slot that holds it
+    for row in range(xrows):
+        for ch in range(nch):
+            a = row * rsb + ((ch ^ (row & 15)) << 4)
+            assert a + 16 <= tile
+            rr, hch, r = held[a]
+            assert r == row and rr == row and hch == ch, (row, ch, held[a])
+    # a fragment read: lanes j = 0..15 of one quarter read rows j at one chunk
+    if xrows >= 16:
+        for ch in range(0, nch, 3):
+            banks = {((j * rsb + ((ch ^ j) << 4)) // 16) % 16 for j in range(16)}
+            assert len(banks) == 16
