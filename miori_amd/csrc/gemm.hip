@@ -40,7 +40,7 @@
 //  * Fused 4-bit B is dequantised to bf16_rne(q*s + b), the exact bf16 value
 //    the dequant kernels write, so the MFMA operands equal the two-step
 //    path's, and so do the results wherever the two-step product runs on
-//    gemm_kernel (its 256x256, 192x256 and small-grid tiles).
+//    gemm_kernel (its small-grid tiles).
 //  * Workgroups are renumbered so each XCD (workgroup id mod 8) works on a
 //    contiguous block of output tiles and keeps its operand slabs in its own
 //    L2. The epilogue stages the fp32 tile through LDS so every lane stores
@@ -741,7 +741,7 @@ __global__ __launch_bounds__(512) void gemm_pc_kernel(
 //  * Rows past N load zeros (buffer loads out of range) and are never stored.
 // The MFMA operands and their order per output are those of gemm_kernel, so
 // results are bit-identical with the two-step dequant + bf16 GEMM wherever
-// that runs on gemm_kernel (256x256, 192x256 and small-grid tiles).
+// that runs on gemm_kernel (its small-grid tiles).
 template <int BM>
 struct CfgQ {  // wave tile of the fused register-B form, for the epilogue
     static constexpr int WM = BM, WN = 32, TM = BM / 32, TN = 1;
