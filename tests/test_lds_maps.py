@@ -149,3 +149,21 @@ def test_skinny_x_tile_map(KB, nloc, xrows):
         for ch in range(0, nch, 3):
             banks = {((j * rsb + ((ch ^ j) << 4)) // 16) % 16 for j in range(16)}
             assert len(banks) == 16
+
+
+@pytest.mark.parametrize("rows,nfrag", [(256, 8), (128, 4), (64, 2)])
+def test_mfma32_fragment_map(rows, nfrag):
+    """The 32x32x16 fragment reads of gemm_kernel and gemm_pcq_kernel: in
+    k-step ks (four per 64-deep K tile) lane half h = lane / 32 reads chunk
+    4h + ks of row (lane % 32) + 32 i, at chunk (4h ^ f) ^ ks with f the
+    row's swizzle term. LDS serves 16 lanes at a time; each group of 16
+    reads 16 rows of one chunk column."""
+    region = (0, rows * ROWB)
+    for ks in range(4):
+        def c0(lane):
+            return (4 * (lane >> 5)) ^ ((lane & 7) ^ ((lane >> 3) & 1))
+        for i in range(nfrag):
+            _check_frag_reads(
+                lambda lane: ((c0(lane) ^ ks) << 4) + (lane & 31) * ROWB + i * 32 * ROWB,
+                lambda lane: 32 * i + (lane & 31), region,
+                lambda lane: 4 * (lane >> 5) + ks)
