@@ -167,3 +167,27 @@ def test_mfma32_fragment_map(rows, nfrag):
                 lambda lane: ((c0(lane) ^ ks) << 4) + (lane & 31) * ROWB + i * 32 * ROWB,
                 lambda lane: 32 * i + (lane & 31), region,
                 lambda lane: 4 * (lane >> 5) + ks)
+
+
+@pytest.mark.parametrize("K,rows", [(2048, 16), (2048, 32), (1024, 9), (4096, 16)])
+def test_lm_head_x_tile_map(K, rows):
+    """The persistent 8-bit lm_head kernel's x tile (skinny.hip lmh_kernel):
+    row r at r * 2K bytes, 1 KiB DMA ch of row r fills chunks ch*64 .. +63,
+    lane l fetching logical chunk ch*64 + (l ^ (r & 15)); a read of logical
+    chunk L (a block's base, a multiple of 16 chunks, plus an offset below
+    16) addresses chunk L ^ (r & 15)."""
+    XR = 2 * K
+    held = {}
+    for r in range(rows):
+        for ch in range(K // 512):
+            for lane in range(64):
+                held[r * XR + ch * 1024 + lane * 16] = (r, ch * 64 + (lane ^ (r & 15)))
+    assert len(held) == rows * K // 8
+    for r in range(rows):
+        for L in range(K // 8):
+            a = r * XR + ((L ^ (r & 15)) << 4)
+            assert held[a] == (r, L)
+    if rows >= 16:
+        for L in range(0, K // 8, 5):
+            banks = {((j * XR + ((L ^ j) << 4)) // 16) % 16 for j in range(16)}
+            assert len(banks) == 16
