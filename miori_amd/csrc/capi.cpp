@@ -15,9 +15,10 @@ using namespace miori;
 namespace {
 
 constexpr uint64_t kMaxBytes = 0xFFFFFFF0ull;
-// Clock sampler bounds: at most 2^20 samples and 2 s of wall clock (100 MHz).
+// Clock sampler bounds: at most 2^20 samples and 2 s of wall clock (the tick
+// limit follows from the device's wall-clock rate).
 constexpr uint32_t kClockMaxSamples = 1u << 20;
-constexpr uint64_t kClockMaxTicks = 200000000ull;
+constexpr uint64_t kClockMaxMs = 2000;
 // miori_linear_q4 takes the exact 4-bit batched GEMV up to this many rows.
 constexpr uint32_t kLinearExactMaxM = 32;
 
@@ -252,14 +253,14 @@ int miori_dequant_q8(const void* q, const void* scales, const void* biases, void
 int miori_diag_clock_sample(uint64_t* samples, uint32_t n, uint32_t gap_ticks,
                             uint32_t* wall_khz, miori_stream stream) {
     if (!samples || !wall_khz) return MIORI_E_NULL;
-    if (n == 0 || gap_ticks == 0 || n > kClockMaxSamples ||
-        (uint64_t)n * gap_ticks > kClockMaxTicks)
-        return MIORI_E_SHAPE;
+    if (n == 0 || gap_ticks == 0 || n > kClockMaxSamples) return MIORI_E_SHAPE;
     if (!aligned(samples, 8)) return MIORI_E_ALIGN;
     int dev = 0, khz = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess)
+        hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0)
         return MIORI_E_HIP;
+    // ticks in 2 s at this device's wall-clock rate (kHz = ticks per ms)
+    if ((uint64_t)n * gap_ticks > kClockMaxMs * (uint64_t)khz) return MIORI_E_SHAPE;
     *wall_khz = (uint32_t)khz;
     return hip_status(launch_clock_sampler(samples, n, gap_ticks, (hipStream_t)stream));
 }

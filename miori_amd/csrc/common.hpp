@@ -4,6 +4,9 @@
 #include <stdlib.h>
 #include <stdint.h>
 
+#include <atomic>
+#include <mutex>
+
 namespace miori {
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -174,6 +177,25 @@ inline int tuning_env(const char* name, int dflt) {
     const char* v = getenv(name);
     return (v && *v) ? atoi(v) : dflt;
 }
+
+// Per-device set-up run once (a kernel attribute, a device property), safe
+// against host threads making their first call on a device together: the
+// first caller runs f under a lock and later callers see the flag. A failed
+// f is retried by the next call.
+struct PerDeviceOnce {
+    std::atomic<bool> done[64] = {};
+    std::mutex mu;
+    template <class F>
+    hipError_t run(int dev, F&& f) {
+        if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+        if (done[dev].load(std::memory_order_acquire)) return hipSuccess;
+        std::lock_guard<std::mutex> g(mu);
+        if (done[dev].load(std::memory_order_relaxed)) return hipSuccess;
+        const hipError_t e = f();
+        if (e == hipSuccess) done[dev].store(true, std::memory_order_release);
+        return e;
+    }
+};
 
 // ---- direct-to-LDS DMA and barriers (gfx950)
 typedef __attribute__((address_space(3))) void* lds_ptr_t;

@@ -670,26 +670,33 @@ __global__ __launch_bounds__(512) void gemm_pc_kernel(
         const uint32_t fsw = (lane & 7u) ^ ((lane >> 3) & 1u);
         const uint32_t c0 = (2u * (lane >> 4)) ^ fsw;
         const uint32_t lrow = (lane & 15u) * ROWB;
-        auto read_frags = [&](uint32_t kt, int ks, int slot) {
+        auto frag_base = [&](uint32_t kt, int ks, bool b) {
             const uint32_t chunk = ((c0 ^ (uint32_t)ks) << 4) + lrow;
-            const uint32_t a_addr = CF::A_OFF + (kt % 3u) * CF::A_ST + wm * CF::WM * ROWB + chunk;
-            const uint32_t b_addr = CF::B_OFF + (kt % 3u) * CF::B_ST + wn * CF::WN * ROWB + chunk;
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-                asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(af[slot][i]) : "v"(a_addr), "i"(i * 16 * ROWB));
+            return b ? CF::B_OFF + (kt % 3u) * CF::B_ST + wn * CF::WN * ROWB + chunk
+                     : CF::A_OFF + (kt % 3u) * CF::A_ST + wm * CF::WM * ROWB + chunk;
+        };
+        auto read_b = [&](uint32_t kt, int ks, int slot) {
+            const uint32_t b_addr = frag_base(kt, ks, true);
 #pragma unroll
             for (int j = 0; j < TN; ++j)
                 asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(bf[slot][j]) : "v"(b_addr), "i"(j * 16 * ROWB));
         };
-        constexpr int NFR = TM + TN;
-        // One k-step's reads fit the lgkm counter's 15. At the top of each
-        // K tile the next k-step's 12 reads are issued while the current
-        // one's 12 may still be in flight (24). gemm_w8_kernel keeps at most
-        // 15 in flight and runs the same fragment map and MFMA order; the
-        // two give bit-identical products on the GPU
-        // (test_gemm_eight_wave_matches_producer_consumer), and both pass
-        // the fp64 oracle checks.
-        static_assert(NFR <= 15, "one k-step's reads fit the lgkm counter");
+        auto read_a = [&](uint32_t kt, int ks, int slot) {
+            const uint32_t a_addr = frag_base(kt, ks, false);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+                asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(af[slot][i]) : "v"(a_addr), "i"(i * 16 * ROWB));
+        };
+        auto read_first = [&](uint32_t kt, int ks, int slot) {
+            read_b(kt, ks, slot);
+            read_a(kt, ks, slot);
+        };
+        auto read_next = [&](uint32_t kt, int ks, int slot) {
+            if constexpr (TM + TN + TN > 15) asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(15 - TN) : "memory");
+            read_b(kt, ks, slot);
+            asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(TN) : "memory");
+            read_a(kt, ks, slot);
+        };
         auto mfmas = [&](int slot) {
 #pragma unroll
             for (int i = 0; i < TM; ++i)
@@ -699,17 +706,16 @@ __global__ __launch_bounds__(512) void gemm_pc_kernel(
                                                                         acc[i][j], 0, 0, 0);
         };
         barrier_lds();  // tile 0 has landed
-        read_frags(0, 0, 0);
+        read_first(0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
         for (uint32_t kt = 0; kt < KT; ++kt) {
-            read_frags(kt, 1, 1);
-            asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(NFR) : "memory");  // k-step 0 has landed
+            read_next(kt, 1, 1);  // k-step 0 has landed
             __builtin_amdgcn_sched_barrier(0);
             mfmas(0);
             __builtin_amdgcn_sched_barrier(0);
             if (kt + 1 < KT) {
                 barrier_lds();  // completes k-step 1's reads; tile kt+1 has landed
-                read_frags(kt + 1, 0, 0);
+                read_first(kt + 1, 0, 0);
             } else {
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             }
@@ -897,6 +903,10 @@ __global__ __launch_bounds__(512) void gemm_pcq_kernel(
             fetch(cl(kt + 2), fx);
 #pragma unroll
             for (int ks = 0; ks < BK / 16 - 1; ++ks) {
+                // at most 15 fragment reads in flight (lgkmcnt's field): with
+                // TM = 8 one of k-step ks's reads lands before the next batch
+                if constexpr (2 * WQ::TM > 15)
+                    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(15 - WQ::TM) : "memory");
                 read_a(kt, ks + 1, (ks + 1) & 1);
                 asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(WQ::TM) : "memory");  // k-step ks has landed
                 __builtin_amdgcn_sched_barrier(0);

@@ -757,29 +757,28 @@ inline size_t lmh_lds_bytes(int mt, uint32_t K, uint32_t G, int nwv) {
 template <int MT, int G, int DEPTH, int NWV>
 hipError_t launch_lmh(const void* X, const void* W, const void* S, const void* B, void* Y,
                       uint32_t M, uint32_t N, uint32_t K, int out_bf16, hipStream_t st) {
-    static int cus[64] = {0};
+    // CU count of each device, and (dynamic LDS above 64 KiB is opted into
+    // once per device, up to the whole 160 KiB) the kernel's LDS attribute
+    static std::atomic<int> cus[64];
+    static PerDeviceOnce setup;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
-    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-    if (cus[dev] == 0) {
+    e = setup.run(dev, [&] {
         int n = 0;
-        e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
-        if (e != hipSuccess) return e;
-        cus[dev] = n;
-    }
-    const size_t lds = lmh_lds_bytes(MT, K, G, NWV);
-    // (dynamic LDS above 64 KiB is opted into once per device, up to the
-    // whole 160 KiB)
-    static bool attr[64] = {false};
-    if (!attr[dev]) {
-        e = hipFuncSetAttribute((const void*)lmh_kernel<MT, G, DEPTH, NWV>,
+        hipError_t r = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+        if (r != hipSuccess) return r;
+        if (n <= 0) return hipErrorInvalidDevice;
+        r = hipFuncSetAttribute((const void*)lmh_kernel<MT, G, DEPTH, NWV>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        if (e != hipSuccess) return e;
-        attr[dev] = true;
-    }
+        if (r == hipSuccess) cus[dev].store(n, std::memory_order_relaxed);
+        return r;
+    });
+    if (e != hipSuccess) return e;
+    const size_t lds = lmh_lds_bytes(MT, K, G, NWV);
     const uint32_t ntiles = (N + 15u) / 16u;
-    const uint32_t grid = std::min<uint32_t>((uint32_t)cus[dev], (ntiles + NWV - 1u) / NWV);
+    const uint32_t grid = std::min<uint32_t>((uint32_t)cus[dev].load(std::memory_order_relaxed),
+                                             (ntiles + NWV - 1u) / NWV);
     hipLaunchKernelGGL((lmh_kernel<MT, G, DEPTH, NWV>), dim3(grid), dim3(NWV * 64), lds, st,
                        (const uint16_t*)X, (const uint8_t*)W, (const uint16_t*)S,
                        (const uint16_t*)B, Y, M, N, K, out_bf16);
@@ -793,12 +792,9 @@ hipError_t launch_sk(const void* X, const void* W, const void* S, const void* B,
     // (the kernel's scale / bias LDS tiles hold 8 blocks per wave)
     if (K / SK / (MODE == Q8X ? 64u : 128u) > 8u * NWV) return hipErrorInvalidValue;
     const uint32_t nwg = (N + 16 * NT - 1) / (16 * NT);
-    float* part = nullptr;
-    if (SK > 1) {
-        const hipError_t e = scratch_get(st, (size_t)SK * M * N * 4, &part);
-        if (e != hipSuccess) return e;
-    }
     using C = Sk<MODE, MT, NT, G, NBW, NWV>;
+    // the shape checks come before the split-K workspace is taken, so a
+    // rejected shape allocates nothing
     size_t xbytes = 0;
     if constexpr (C::XL) {
         // 16-byte aligned rows (K % 8 == 0 and an aligned X, which the C ABI
@@ -810,19 +806,22 @@ hipError_t launch_sk(const void* X, const void* W, const void* S, const void* B,
         if (tile > (size_t)C::XT_MAX) return hipErrorInvalidValue;
         if (xbytes > 64 * 1024) {
             // (dynamic LDS above 64 KiB is opted into once per device)
-            static bool attr[64] = {false};
+            static PerDeviceOnce attr;
             int dev = 0;
             hipError_t e = hipGetDevice(&dev);
             if (e != hipSuccess) return e;
-            if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-            if (!attr[dev]) {
-                e = hipFuncSetAttribute((const void*)skinny_kernel<MODE, MT, NT, G, NBW, NWV>,
-                                        hipFuncAttributeMaxDynamicSharedMemorySize,
-                                        160 * 1024 - C::LDS);
-                if (e != hipSuccess) return e;
-                attr[dev] = true;
-            }
+            e = attr.run(dev, [] {
+                return hipFuncSetAttribute((const void*)skinny_kernel<MODE, MT, NT, G, NBW, NWV>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           160 * 1024 - C::LDS);
+            });
+            if (e != hipSuccess) return e;
         }
+    }
+    float* part = nullptr;
+    if (SK > 1) {
+        const hipError_t e = scratch_get(st, (size_t)SK * M * N * 4, &part);
+        if (e != hipSuccess) return e;
     }
     hipLaunchKernelGGL((skinny_kernel<MODE, MT, NT, G, NBW, NWV>), dim3(nwg, SK, MZ), dim3(NWV * 64),
                        xbytes, st, (const uint16_t*)X, (const uint8_t*)W, (const uint16_t*)S,

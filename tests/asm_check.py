@@ -25,6 +25,18 @@ def _regs(tok):
 
 _WAIT = re.compile(r"(vmcnt|lgkmcnt)\((\d+)\)")
 _CAP = 64  # longest pending queue tracked (hardware counters are smaller)
+# Largest count lgkmcnt's 4-bit field can express on gfx950. A path that
+# leaves more LDS reads (operations that fill registers) outstanding than that
+# relies on how the counter behaves past its field, so it is reported. LDS
+# writes are not counted: the compiler itself issues long runs of them and
+# drains them with a full wait. (vmcnt has 6 bits; the deepest hand-placed
+# vector-load queue here is 32, and loops of LDS DMAs with run-time trip
+# counts make a static vmcnt depth meaningless, so it is not checked.)
+_LG_LIMIT = 15
+
+
+def _loads(q):
+    return sum(1 for regs, _ in q if regs)
 
 
 def _parse(lines):
@@ -185,6 +197,8 @@ def _step(state, ln, s, bad):
             vm = (vm + (entry,))[-_CAP:]
         if "lg" in cls[0]:
             lg = (lg + (entry,))[-_CAP:]
+            if dest and _loads(lg) > _LG_LIMIT:
+                bad.append((ln, s, "lgkmcnt overflow"))
     return (vm, lg, consts)
 
 

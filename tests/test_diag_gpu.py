@@ -59,3 +59,13 @@ def test_clock_sampler_beside_gemm(dev):
     _check(buf, khz, n, gap)
     ref = A.float() @ B.float().t()
     assert ((C.float() - ref).abs().max() / ref.abs().max()).item() < 1e-2
+
+
+def test_clock_sampler_rejects_more_than_two_seconds(dev):
+    # the bound is 2 s at the device's own wall-clock rate: 2^20 samples 1 ms
+    # apart is far over it on any part
+    khz = ctypes.c_uint32(0)
+    say("clock sampler bound")
+    rc = _lib.status("miori_diag_clock_sample", ctypes.c_void_p(1 << 20), 1 << 20, 10**6,
+                     ctypes.byref(khz), None)
+    assert rc == -2
