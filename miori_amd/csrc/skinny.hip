@@ -236,7 +236,7 @@ template <int MODE, int MT, int NT, int G, int NBW, int NWV>
 __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
     const uint16_t* __restrict__ X, const uint8_t* __restrict__ W,
     const uint16_t* __restrict__ S, const uint16_t* __restrict__ Bi, void* __restrict__ Y,
-    uint32_t M, uint32_t N, uint32_t K, int out_bf16, float* __restrict__ part) {
+    uint32_t M, uint32_t N, uint32_t K, int out_bf16, float* __restrict__ part, uint32_t xrot) {
     using C = Sk<MODE, MT, NT, G, NBW, NWV>;
     // scale / bias tiles first, the cross-wave reduction buffer at the end
     __shared__ __attribute__((aligned(1024))) uint8_t lds[C::LDS];
@@ -298,7 +298,13 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
     if constexpr (C::XL) {
         const uint32_t nins = (xrows * rsb + 1023u) / 1024u;
         const uint32_t nch = nloc * C::KB / 8u;
-        for (uint32_t u = wave; u < nins; u += NWV) {
+        // xrot != 0: the workgroups of one XCD (blockIdx.x % 8 alike) start
+        // at chunks spread over the tile, so they do not all fetch the same
+        // lines at the same moment (the same DMAs, in a rotated order)
+        const uint32_t per_xcd = max(1u, gridDim.x >> 3);
+        const uint32_t r0 = xrot ? (blockIdx.x >> 3) % per_xcd * nins / per_xcd : 0u;
+        for (uint32_t v = wave; v < nins; v += NWV) {
+            const uint32_t u = v + r0 < nins ? v + r0 : v + r0 - nins;
             const uint32_t p = u * 1024u + lane * 16u;
             const uint32_t r = p / rsb;
             const uint32_t rr = min(r, xrows - 1u);
@@ -589,7 +595,7 @@ __global__ __launch_bounds__(NWV * 64) void lmh_kernel(const uint16_t* __restric
                                                   const uint16_t* __restrict__ S,
                                                   const uint16_t* __restrict__ Bi,
                                                   void* __restrict__ Y, uint32_t M, uint32_t N,
-                                                  uint32_t K, int out_bf16) {
+                                                  uint32_t K, int out_bf16, uint32_t xrot) {
     constexpr int KB = 64;
     static_assert(G == 64 || G == 128, "one scale / bias per 64-k block");
     extern __shared__ __attribute__((aligned(16))) uint8_t xs[];
@@ -608,7 +614,12 @@ __global__ __launch_bounds__(NWV * 64) void lmh_kernel(const uint16_t* __restric
     // the 16 rows of an MFMA fragment read fall on distinct banks; the DMA
     // writes lanes in order, so each lane fetches the chunk its slot holds.
     const uint32_t nch = K / 512u;
-    for (uint32_t u = wave; u < rows * nch; u += NWV) {
+    // xrot != 0: each workgroup starts at a different DMA of the tile (the
+    // same DMAs, rotated), so the CUs do not fetch the same lines together
+    const uint32_t nx = rows * nch;
+    const uint32_t r0 = xrot ? (blockIdx.x * 37u) % nx : 0u;
+    for (uint32_t v = wave; v < nx; v += NWV) {
+        const uint32_t u = v + r0 < nx ? v + r0 : v + r0 - nx;
         const uint32_t r = u / nch, ch = u % nch;
         dma16(X + (size_t)r * K + (ch * 64u + (lane ^ (r & 15u))) * 8u, xs + r * XR + ch * 1024u);
     }
@@ -776,12 +787,13 @@ hipError_t launch_lmh(const void* X, const void* W, const void* S, const void* B
     });
     if (e != hipSuccess) return e;
     const size_t lds = lmh_lds_bytes(MT, K, G, NWV);
+    static const uint32_t xrot = (uint32_t)tuning_env("MIORI_SKINNY_XROT", 0);
     const uint32_t ntiles = (N + 15u) / 16u;
     const uint32_t grid = std::min<uint32_t>((uint32_t)cus[dev].load(std::memory_order_relaxed),
                                              (ntiles + NWV - 1u) / NWV);
     hipLaunchKernelGGL((lmh_kernel<MT, G, DEPTH, NWV>), dim3(grid), dim3(NWV * 64), lds, st,
                        (const uint16_t*)X, (const uint8_t*)W, (const uint16_t*)S,
-                       (const uint16_t*)B, Y, M, N, K, out_bf16);
+                       (const uint16_t*)B, Y, M, N, K, out_bf16, xrot);
     return hipGetLastError();
 }
 
@@ -823,9 +835,12 @@ hipError_t launch_sk(const void* X, const void* W, const void* S, const void* B,
         const hipError_t e = scratch_get(st, (size_t)SK * M * N * 4, &part);
         if (e != hipSuccess) return e;
     }
+    // (MIORI_SKINNY_XROT=1: rotated x-tile DMA order per workgroup, a tuning
+    // experiment, off by default)
+    static const uint32_t xrot = (uint32_t)tuning_env("MIORI_SKINNY_XROT", 0);
     hipLaunchKernelGGL((skinny_kernel<MODE, MT, NT, G, NBW, NWV>), dim3(nwg, SK, MZ), dim3(NWV * 64),
                        xbytes, st, (const uint16_t*)X, (const uint8_t*)W, (const uint16_t*)S,
-                       (const uint16_t*)B, Y, M, N, K, out_bf16, part);
+                       (const uint16_t*)B, Y, M, N, K, out_bf16, part, xrot);
     if (SK > 1) {
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;

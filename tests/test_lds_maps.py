@@ -191,3 +191,21 @@ def test_lm_head_x_tile_map(K, rows):
         for L in range(0, K // 8, 5):
             banks = {((j * XR + ((L ^ j) << 4)) // 16) % 16 for j in range(16)}
             assert len(banks) == 16
+
+
+@pytest.mark.parametrize("nins,grid", [(128, 256), (33, 256), (7, 64), (128, 8), (5, 3)])
+def test_rotated_x_dma_order_covers_tile(nins, grid):
+    """MIORI_SKINNY_XROT: the skinny kernel's x-tile DMAs in rotated order
+    (start r0 = (blockIdx / 8) % per_xcd * nins / per_xcd, wave w taking
+    v = w, w + 8, ... and DMA u = (v + r0) mod nins), and lmh_kernel's
+    (r0 = blockIdx * 37 mod nx): every DMA of the tile issued exactly once
+    per workgroup, so the tile's contents do not depend on the order."""
+    per_xcd = max(1, grid >> 3)
+    for bid in range(grid):
+        for r0 in ((bid >> 3) % per_xcd * nins // per_xcd, (bid * 37) % nins):
+            assert 0 <= r0 < nins
+            us = []
+            for w in range(8):
+                for v in range(w, nins, 8):
+                    us.append(v + r0 if v + r0 < nins else v + r0 - nins)
+            assert sorted(us) == list(range(nins))
