@@ -73,6 +73,12 @@ __device__ __forceinline__ void asm_load_u16(uint32_t& d, rsrc_t r, uint32_t off
 }
 __device__ __forceinline__ void tie(u32x4_t& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void tie(uint32_t& v) { asm volatile("" : "+v"(v)); }
+// After the wait that covers a slot's LDS fragment reads, the slot's
+// registers are tied before its MFMAs: each read's output then stays live
+// until that point, so the compiler cannot give its register to other code
+// while the read is still in flight (it would if the output were dead, as in
+// a build with the MFMAs compiled out, which faulted the GPU).
+__device__ __forceinline__ void tie(bf16x8_t& v) { asm volatile("" : "+v"(v)); }
 
 template <int BM, int BN, bool Q4, int G>
 struct Cfg {
@@ -420,6 +426,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     };
     auto mfmas = [&](int slot) {
 #pragma unroll
+        for (int i = 0; i < CF::TM; ++i) tie(af[slot][i]);
+#pragma unroll
+        for (int j = 0; j < CF::TN; ++j) tie(bf[slot][j]);
+#pragma unroll
         for (int i = 0; i < CF::TM; ++i)
 #pragma unroll
             for (int j = 0; j < CF::TN; ++j)
@@ -436,6 +446,10 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     auto mfmas_dma = [&](int slot, bool dma, uint32_t dkt, uint32_t dst, auto p0c, auto p1c) {
         constexpr int P0 = decltype(p0c)::value, P1 = decltype(p1c)::value;
         constexpr int CNT = P1 - P0;
+#pragma unroll
+        for (int i = 0; i < CF::TM; ++i) tie(af[slot][i]);
+#pragma unroll
+        for (int j = 0; j < CF::TN; ++j) tie(bf[slot][j]);
 #pragma unroll
         for (int q = 0; q < NM; ++q) {
             const int i = q / CF::TN, j = q % CF::TN;
@@ -699,6 +713,10 @@ __global__ __launch_bounds__(512) void gemm_pc_kernel(
         };
         auto mfmas = [&](int slot) {
 #pragma unroll
+            for (int i = 0; i < TM; ++i) tie(af[slot][i]);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) tie(bf[slot][j]);
+#pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
                 for (int j = 0; j < TN; ++j)
@@ -877,6 +895,9 @@ __global__ __launch_bounds__(512) void gemm_pcq_kernel(
             fbi = bf16_bits_to_f32(x.bi);
         };
         auto make_b = [&](const Codes& x, int ks, int slot) { bq[slot] = deq(x.raw[ks], fsc, fbi); };
+        // (no ties here: they reorder this kernel's MFMA / dequant interleave;
+        // every fragment feeds an MFMA of its own k-step, checked by the
+        // hazard test on the compiled kernel)
         auto mfmas = [&](int slot) {
 #pragma unroll
             for (int i = 0; i < WQ::TM; ++i)
@@ -1075,6 +1096,9 @@ __global__ __launch_bounds__(512) void gemm_w8_kernel(
         asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(TN) : "memory");
         read_a(kt, ks, slot);
     };
+    // (no ties here: they change this kernel's register allocation and LDS
+    // read order; every fragment feeds an MFMA of its own k-step, checked by
+    // the hazard test on the compiled kernel)
     auto mfmas_dma = [&](int slot, bool dma, uint32_t dkt, uint32_t dst) {
         constexpr int NM = TM * TN;
 #pragma unroll
