@@ -83,8 +83,8 @@ def _parse():
     p.add_argument("--headline-only", action="store_true",
                    help="only the config-0 GEMV and the launch floors (for counter passes)")
     p.add_argument("--case", default=None,
-                   help="time one case only, KIND,M,N,K with KIND gemv4 | gemv8 | gemm_bf16 | "
-                        "gemm_q4 (for profiling runs)")
+                   help="time one case only, KIND,M,N,K with KIND gemv4 | gemv8 | gemv4b | gemv8b "
+                        "(batched entry at any M) | gemm_bf16 | gemm_q4 (for profiling runs)")
     p.add_argument("--clock", action="store_true",
                    help="also sample the shader clock during a GEMM replay (a side-stream "
                         "kernel; off by default)")
@@ -119,8 +119,10 @@ class Timer:
         self.flush.add_(1)  # reads and writes 1 GiB (about 0.3 ms)
         self.flush.add_(1)
 
-    def run(self, fn, steps, warmup):
-        """Return (ms for `steps` launches, mode)."""
+    def run(self, fn, steps, warmup, pre=None):
+        """Return (ms for `steps` launches, mode). `pre` (optional) is
+        enqueued between the flush and the timed replay, e.g. to bring an
+        operand back into the caches."""
         torch = self.torch
         for i in range(warmup):
             fn(i)
@@ -137,6 +139,8 @@ class Timer:
         # it, the host submits the timed replay, so the host-side graph
         # launch cost stays outside the events.
         self._flush()
+        if pre is not None:
+            pre()
         s0.record()
         g.replay()
         s1.record()
@@ -227,9 +231,9 @@ class Ctx:
         self.gen.manual_seed(0x4D494F52)
 
 
-def gemv_row(c, bits, M, N, K, G=64, steps=None, hot=False, tag=None):
-    """Configs 0-2: the exact 4/8-bit GEMV (M = 1) or batched GEMV (M > 1),
-    bf16 out, on rotating weight copies."""
+def gemv_row(c, bits, M, N, K, G=64, steps=None, hot=False, tag=None, batched=False):
+    """Configs 0-2: the exact 4/8-bit GEMV (M = 1) or batched GEMV (M > 1, or
+    any M with `batched`), bf16 out, on rotating weight copies."""
     torch, ops = c.torch, c.ops
     steps = steps or c.steps
     if bits == 8 and N >= 65536:
@@ -248,7 +252,7 @@ def gemv_row(c, bits, M, N, K, G=64, steps=None, hot=False, tag=None):
 
     def fn(i):
         j = i % copies
-        if M == 1:
+        if M == 1 and not batched:
             f1(qs[j], ss[j], bs[j], x, y, N, K, group=G)
         else:
             fb(qs[j], ss[j], bs[j], x, y, N, K, M, group=G)
@@ -265,6 +269,13 @@ def gemv_row(c, bits, M, N, K, G=64, steps=None, hot=False, tag=None):
     if hot:
         th, _ = c.timer.run(lambda i: fn(0), steps, c.warmup)
         row["hot_cache_us"] = round(th * 1e3 / steps, 3)
+    if M > 1:
+        # x in the caches, weights still cold: a decode step finds x fresh
+        # from the kernel that produced it, while the flush above evicts it
+        # from L2 and the Infinity Cache like the weights
+        xi = x.view(torch.int16)
+        tx, _ = c.timer.run(fn, steps, 1, pre=lambda: xi.add_(0))
+        row["x_hot_us"] = round(tx * 1e3 / steps, 3)
     del qs, ss, bs
     torch.cuda.empty_cache()
     return row
@@ -602,6 +613,10 @@ def main():
         M, N, K = int(M), int(N), int(K)
         if kind in ("gemv4", "gemv8"):
             row = gemv_row(c, 4 if kind == "gemv4" else 8, M, N, K)
+        elif kind in ("gemv4b", "gemv8b"):
+            # the batched entry point at any M (with MIORI_BATCH_MFMA_MIN_M
+            # this times the MFMA kernel at M < 5)
+            row = gemv_row(c, 4 if kind == "gemv4b" else 8, M, N, K, batched=True)
         elif kind in ("gemm_bf16", "gemm_q4"):
             row = gemm_row(c, M, N, K, kind == "gemm_q4", steps=min(args.steps, 30),
                            vendor=args.clock and kind == "gemm_bf16", clock=args.clock)
