@@ -110,14 +110,19 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(
     static_assert(RV0 <= 16, "at most 16 row sums per wave");
     __shared__ float red[4][RV];
 
+    // Index arithmetic in scalar registers where it is wave-uniform, and by
+    // shifts: S (1, 2 or 4) and G (16..128) are powers of two, checked by
+    // the callers, so no integer division is emitted and the first weight
+    // load issues after a few instructions.
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wave = threadIdx.x >> 6;
-    const uint32_t js = wave % S;   // K slice handled by this wave
-    const uint32_t rb = wave / S;   // row block inside the workgroup
-    const uint32_t rows_per_wg = R * (4u / S);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t lgS = (uint32_t)__builtin_ctz(S), lgG = (uint32_t)__builtin_ctz(G);
+    const uint32_t js = wave & (S - 1u);  // K slice handled by this wave
+    const uint32_t rb = wave >> lgS;      // row block inside the workgroup
+    const uint32_t rows_per_wg = R * (4u >> lgS);
     const uint32_t row0 = blockIdx.x * rows_per_wg + rb * R;
     const uint32_t C = K / E;       // chunks per row
-    const uint32_t ng = K / G;
+    const uint32_t ng = K >> lgG;
 
     const rsrc_t rq = make_rsrc(q, N * C * 16u);
     const rsrc_t rs = make_rsrc(s, N * ng * 2u);
@@ -191,7 +196,7 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(
         for (int i = 0; i < CPL; ++i) {
             const bool ok = rv && cval[i];
             qv[r][i] = buf_load16_aux<kQAux>(rq, ok ? (row * C + cidx[i]) * 16u : kOOB);
-            const uint32_t g = cidx[i] * E / G;
+            const uint32_t g = (cidx[i] * E) >> lgG;
             const uint32_t so = ok ? (row * ng + g) * 2u : kOOB;
             sv[r][i] = buf_load_u16_aux<kSbAux>(rs, so);
             bv[r][i] = buf_load_u16_aux<kSbAux>(rb_, so);
