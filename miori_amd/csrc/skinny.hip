@@ -292,7 +292,7 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
         const uint32_t row = min(mt * 16u + j, xrows - 1u);
-        xrb[mt] = row * rsb;
+        xrb[mt] = __umul24(row, rsb);
         xsw[mt] = row & 15u;
     }
     if constexpr (C::XL) {
@@ -303,13 +303,24 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
         // lines at the same moment (the same DMAs, in a rotated order)
         const uint32_t per_xcd = max(1u, gridDim.x >> 3);
         const uint32_t r0 = xrot ? (blockIdx.x >> 3) % per_xcd * nins / per_xcd : 0u;
+        // The row of a lane's 16-byte slot p is p / rsb. rsb is a multiple of
+        // 256 bytes, so r = floor(a / d) with a = p / 256 and d = rsb / 256,
+        // computed in fp32 as trunc((a + 1/2) / d): that quotient lies at
+        // least 1/(2d) >= 2^-7 from an integer, and its rounding error is
+        // below a * 2^-23 <= 2^-12 (a < 2^11, d <= 64). This replaces an
+        // integer division (about 20 VALU instructions, five of them
+        // quarter-rate) per DMA with four full-rate ones; the offsets fit
+        // 24-bit multiplies (r < 2^11, rsb <= 2^14; x rows < 32, K <= 2^15).
+        const float inv_d = 1.0f / (float)(rsb >> 8);
+        const uint32_t xoff0 = __umul24(m0, K) + kbase;
         for (uint32_t v = wave; v < nins; v += NWV) {
             const uint32_t u = v + r0 < nins ? v + r0 : v + r0 - nins;
             const uint32_t p = u * 1024u + lane * 16u;
-            const uint32_t r = p / rsb;
+            const uint32_t a = u * 4u + (lane >> 4);
+            const uint32_t r = (uint32_t)(((float)a + 0.5f) * inv_d);
             const uint32_t rr = min(r, xrows - 1u);
-            const uint32_t ch = min(((p - r * rsb) >> 4) ^ (r & 15u), nch - 1u);
-            dma16(X + (size_t)(m0 + rr) * K + kbase + ch * 8u, xdyn + u * 1024u);
+            const uint32_t ch = min(((p - __umul24(r, rsb)) >> 4) ^ (r & 15u), nch - 1u);
+            dma16(X + (xoff0 + __umul24(rr, K) + ch * 8u), xdyn + u * 1024u);
         }
     }
 

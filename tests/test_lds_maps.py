@@ -6,6 +6,7 @@ serves together hit 16 distinct 16-byte bank groups. The formulas restate
 the index arithmetic of gemm_w8_kernel, gemm_pc_kernel (miori_amd/csrc/
 gemm.hip) and the skinny kernel's x tile (miori_amd/csrc/skinny.hip); a
 change to one of them that breaks a mapping fails here before any GPU run."""
+import numpy as np
 import pytest
 
 ROWB = 128  # bytes per LDS row of a bf16 K tile (64 elements)
@@ -129,10 +130,14 @@ def test_skinny_x_tile_map(KB, nloc, xrows):
     nins = (xrows * rsb + 1023) // 1024
     tile = nins * 1024
     held = {}
+    inv_d = np.float32(1.0) / np.float32(rsb >> 8)
     for u in range(nins):
         for lane in range(64):
             p = u * 1024 + lane * 16
-            r = p // rsb
+            # the kernel's division-free row: trunc((a + 1/2) * (1/d)) in fp32
+            a = u * 4 + (lane >> 4)
+            r = int((np.float32(a) + np.float32(0.5)) * inv_d)
+            assert r == p // rsb
             rr = min(r, xrows - 1)
             ch = min(((p - r * rsb) >> 4) ^ (r & 15), nch - 1)
             assert p + 16 <= tile
@@ -209,3 +214,15 @@ def test_rotated_x_dma_order_covers_tile(nins, grid):
                 for v in range(w, nins, 8):
                     us.append(v + r0 if v + r0 < nins else v + r0 - nins)
             assert sorted(us) == list(range(nins))
+
+
+def test_fp32_row_division_exhaustive():
+    """The skinny kernel's x-tile DMA loop takes a slot's row as
+    trunc((a + 1/2) * fp32(1/d)) instead of a // d (a = slot / 256 bytes,
+    d = row bytes / 256). Every a < 2^11 and d <= 64 the kernel can see
+    (x tile <= 32 rows of <= 16 KiB) gives the integer quotient."""
+    a = np.arange(1 << 11, dtype=np.int64)
+    for d in range(1, 65):
+        inv = np.float32(1.0) / np.float32(d)
+        q = ((a.astype(np.float32) + np.float32(0.5)) * inv).astype(np.int64)
+        assert np.array_equal(q, a // d), d
