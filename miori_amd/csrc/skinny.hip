@@ -254,7 +254,9 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
     const uint32_t n0 = blockIdx.x * 16u * NT;
     const uint32_t nblk = K / C::KB;
     // this workgroup's K blocks: [kb0, kb0 + nloc) (split gridDim.y ways)
-    const uint32_t nloc = nblk / gridDim.y, kb0 = blockIdx.y * nloc;
+    // (the unsplit launches skip the integer divisions: gridDim.y and
+    // gridDim.z are uniform, so these are scalar branches)
+    const uint32_t nloc = gridDim.y == 1 ? nblk : nblk / gridDim.y, kb0 = blockIdx.y * nloc;
     const uint32_t b0 = kb0 + wave * nloc / NWV, b1 = kb0 + (wave + 1) * nloc / NWV;
     const uint32_t nb = b1 - b0;
     const uint32_t ng = (MODE == BF16) ? 1u : K / G;
@@ -271,7 +273,7 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
     const uint16_t* xrow[MT];
     // rows [m0, m0 + mstep) of y (M split over gridDim.z); x rows past that
     // range are loaded (clamped into x) but their outputs are not stored
-    const uint32_t mstep = (M + gridDim.z - 1) / gridDim.z;
+    const uint32_t mstep = gridDim.z == 1 ? M : (M + gridDim.z - 1) / gridDim.z;
     const uint32_t m0 = blockIdx.z * mstep;
     const uint32_t m1 = min(M, m0 + mstep);
 #pragma unroll
