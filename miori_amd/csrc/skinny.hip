@@ -180,6 +180,9 @@ __device__ __forceinline__ void buf16_at(u32x4_t& d, rsrc_t r, uint32_t off) {
 // an offset past any buffer of the persistent kernel (N * K < 2^31) even
 // with the largest immediate added
 constexpr uint32_t kLmhOOB = 0x80000000u;
+// an x-row offset past the skinny kernel's x buffer (M * K * 2 <= 512 KiB)
+// however far into a row a load reaches (K * 2 <= 16 KiB)
+constexpr uint32_t kXOOB = 0x80000000u;
 __device__ __forceinline__ void ld8(u32x2_t& d, const void* p) {
     asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(d) : "v"(p));
 }
@@ -270,14 +273,23 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
         const size_t rb = (MODE == Q4X || MODE == Q4F) ? K / 2 : (MODE == Q8X ? K : 2ull * K);
         wrow[nt] = W + (size_t)n * rb;
     }
-    const uint16_t* xrow[MT];
+    // x rows as byte offsets into a buffer over x (loads per block, forms
+    // without the LDS x tile): rows outside the workgroup's range [m0, m1)
+    // take an out-of-range offset and read as zeros without touching memory
+    // (their outputs are never stored; each output row depends only on its
+    // own x row)
+    uint32_t xro[MT];
     // rows [m0, m0 + mstep) of y (M split over gridDim.z); x rows past that
     // range are loaded (clamped into x) but their outputs are not stored
     const uint32_t mstep = gridDim.z == 1 ? M : (M + gridDim.z - 1) / gridDim.z;
     const uint32_t m0 = blockIdx.z * mstep;
     const uint32_t m1 = min(M, m0 + mstep);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) xrow[mt] = X + (size_t)min(m0 + mt * 16u + j, M - 1u) * K;
+    for (int mt = 0; mt < MT; ++mt) {
+        const uint32_t m = m0 + mt * 16u + j;
+        xro[mt] = m < m1 ? m * K * 2u : kXOOB;
+    }
+    const rsrc_t rx = make_rsrc(X, M * K * 2u);
 
     // x tile in LDS (C::XL): rows m0 .. m0+xrows-1 over the workgroup's K
     // range [kbase, kbase + nloc*KB), row r at r * rsb bytes; 16-byte chunk
@@ -349,7 +361,7 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
                 for (int r = 0; r < C::STEPS; ++r)
-                    ld16(xr[sl][mt][r], xrow[mt] + k0 + kmap<MODE, G>(c, r));
+                    buf16_at<0>(xr[sl][mt][r], rx, xro[mt] + 2u * (k0 + kmap<MODE, G>(c, r)));
         }
     };
 
