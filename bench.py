@@ -88,6 +88,9 @@ def _parse():
     p.add_argument("--clock", action="store_true",
                    help="also sample the shader clock during a GEMM replay (a side-stream "
                         "kernel; off by default)")
+    p.add_argument("--diag-gemv", action="store_true",
+                   help="per-wave wall-clock timeline of one cold headline GEMV launch "
+                        "(miori_diag_gemv_q4_timeline), printed as one JSON line")
     p.add_argument("--calib-copy", action="store_true",
                    help="also run a 256 MiB device copy (reference for the HBM byte counters)")
     return p.parse_args()
@@ -492,6 +495,50 @@ def add_floor(row, floors):
     return row
 
 
+def gemv_timeline(c, N=8192, K=2048, G=64, reps=5):
+    """Decompose cold headline GEMV launches with the stamped diagnostic
+    build: per wave, the wall-clock time from the first wave's start to
+    its own start, to its loads landing, to its arithmetic done and to its
+    stores completing. Each launch follows a 1 GiB flush on a fresh weight
+    copy. Percentiles over waves, median over launches."""
+    import numpy as np
+    torch, ops = c.torch, c.ops
+    w = c.synth.quant_weights(N, K, G, 4, seed=c.synth.BASE_SEED + 900)
+    lin = ops.QuantLinear(w, c.dev)
+    x = ops.to_device_bits(c.synth.activations(1, K), c.dev)
+    y = torch.empty(N, dtype=torch.bfloat16, device=c.dev)
+    keys = ("start", "landed", "math_done", "stored")
+    runs = []
+    for r in range(reps):
+        q, s, b = lin.q.clone(), lin.s.clone(), lin.b.clone()
+        torch.cuda.synchronize()
+        c.timer._flush()
+        st = ops.gemv4_timeline(q, s, b, x, y, N, K, group=G)
+        torch.cuda.synchronize()
+        a = st.cpu().numpy().astype(np.int64)
+        a = a - a[:, 0].min()
+        runs.append({k: np.percentile(a[:, i], [0, 10, 50, 90, 100]) for i, k in enumerate(keys)})
+        runs[-1]["compute"] = np.percentile(a[:, 2] - a[:, 1], [0, 10, 50, 90, 100])
+        runs[-1]["after_last_landed"] = a[:, 3].max() - a[:, 1].max()
+    # ticks per microsecond from the device's wall-clock rate
+    import ctypes
+    from miori_amd import _lib
+    khz = ctypes.c_uint32(0)
+    smp = torch.zeros(4, dtype=torch.int64, device=c.dev)
+    _lib.call("miori_diag_clock_sample", ctypes.c_void_p(smp.data_ptr()), 2, 1,
+              ctypes.byref(khz), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    tpu = khz.value / 1000.0
+    out = {"unit": "us from the first wave's start", "wall_clock_kHz": khz.value,
+           "percentiles": [0, 10, 50, 90, 100], "waves": int(a.shape[0]), "launches": reps}
+    for k in keys + ("compute",):
+        med = np.median(np.stack([r[k] for r in runs]), axis=0) / tpu
+        out[k] = [round(float(v), 3) for v in med]
+    out["last_landed_to_last_store_us"] = round(
+        float(np.median([r["after_last_landed"] for r in runs])) / tpu, 3)
+    return out
+
+
 def calib_copy(torch, dev):
     """A plain 256 MiB device copy, three times: it reads and writes exactly
     256 MiB per launch, the reference for scaling FETCH_SIZE / WRITE_SIZE."""
@@ -608,6 +655,9 @@ def main():
         print(f"[bench] {row}", file=sys.stderr, flush=True)
         return row
 
+    if args.diag_gemv:
+        print(json.dumps({"gemv4_timeline": gemv_timeline(c)}), flush=True)
+        return
     if args.case:
         kind, M, N, K = args.case.split(",")
         M, N, K = int(M), int(N), int(K)

@@ -225,6 +225,18 @@ int miori_dequant_q8(const void* q, const void* scales, const void* biases,
  * samples 8-byte aligned device memory. */
 int miori_diag_clock_sample(uint64_t* samples, uint32_t n, uint32_t gap_ticks,
                             uint32_t* wall_khz, miori_stream stream);
+/* No counterpart in the reference. miori_gemv_q4 (M = 1, K <= 2048 and a
+ * multiple of 32) on the same kernel with one extra full load wait, also
+ * writing four wall-clock stamps per wave (s_memrealtime ticks) into
+ * stamps[4w .. 4w+3]: entry, all of the wave's loads landed, arithmetic and
+ * reduction done, stores complete. *nwaves (host pointer) receives the wave
+ * count, ceil(N / 16) * 4; cap is the capacity of stamps in values and must
+ * be >= 4 * nwaves. y is the same as miori_gemv_q4's. For decomposing a
+ * launch's time, not for production. */
+int miori_diag_gemv_q4_timeline(const void* q, const void* scales, const void* biases,
+                                const void* x, void* y, uint32_t N, uint32_t K, uint32_t group,
+                                int out_dtype, uint64_t* stamps, uint32_t cap,
+                                uint32_t* nwaves, miori_stream stream);
 
 #ifdef __cplusplus
 }

@@ -37,6 +37,7 @@ SIGNATURES = {
     "miori_dequant_q4": ([_P, _P, _P, _P, _U, _U, _U, _P], _I),
     "miori_dequant_q8": ([_P, _P, _P, _P, _U, _U, _U, _P], _I),
     "miori_diag_clock_sample": ([_P, _U, _U, _P, _P], _I),
+    "miori_diag_gemv_q4_timeline": ([_P, _P, _P, _P, _P, _U, _U, _U, _I, _P, _U, _P, _P], _I),
 }
 
 _lib = None

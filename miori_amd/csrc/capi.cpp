@@ -265,4 +265,21 @@ int miori_diag_clock_sample(uint64_t* samples, uint32_t n, uint32_t gap_ticks,
     return hip_status(launch_clock_sampler(samples, n, gap_ticks, (hipStream_t)stream));
 }
 
+int miori_diag_gemv_q4_timeline(const void* q, const void* scales, const void* biases,
+                                const void* x, void* y, uint32_t N, uint32_t K, uint32_t group,
+                                int out_dtype, uint64_t* stamps, uint32_t cap,
+                                uint32_t* nwaves, miori_stream stream) {
+    int st = check_gemv(4, q, scales, biases, x, y, 1, N, K, group, out_dtype);
+    if (st) return st;
+    if (!stamps || !nwaves) return MIORI_E_NULL;
+    if (K > 2048) return MIORI_E_SHAPE;
+    if (!aligned(stamps, 8)) return MIORI_E_ALIGN;
+    const uint64_t need = ((uint64_t)N + 15u) / 16u * 16u;
+    *nwaves = (uint32_t)(need / 4u);
+    if (cap < need) return MIORI_E_SHAPE;
+    return hip_status(launch_gemv_q4_timeline(q, scales, biases, x, y, N, K, group,
+                                              out_dtype == MIORI_BF16, stamps, cap, nwaves,
+                                              (hipStream_t)stream));
+}
+
 }  // extern "C"

@@ -97,11 +97,19 @@ __device__ __forceinline__ uint32_t silu_mul_bf16(float a, float u) {
     return f32_to_bf16_bits(v);
 }
 
-template <int BITS, int MR, int R, int CPL, int XM = XM_PLAIN>
+// DIAG = 1 (a diagnostic build, miori_diag_gemv_q4_timeline): each wave
+// also records four wall-clock stamps (s_memrealtime, 100 MHz) into
+// stamps[4 * wave]: at entry, once all its loads have landed (an extra full
+// vmcnt wait), after its arithmetic and reduction, and once its stores have
+// completed. Only for S = 1 (every row in one wave).
+template <int BITS, int MR, int R, int CPL, int XM = XM_PLAIN, int DIAG = 0>
 __global__ __launch_bounds__(256) void gemv_valu_kernel(
     const void* __restrict__ q, const void* __restrict__ s, const void* __restrict__ bs,
     const void* __restrict__ x, void* __restrict__ y, uint32_t N, uint32_t K, uint32_t G,
-    uint32_t S, int out_bf16, const void* __restrict__ x2 = nullptr, float eps = 0.f) {
+    uint32_t S, int out_bf16, const void* __restrict__ x2 = nullptr, float eps = 0.f,
+    uint64_t* __restrict__ stamps = nullptr) {
+    uint64_t t_in = 0, t_land = 0, t_math = 0;
+    if constexpr (DIAG) t_in = __builtin_amdgcn_s_memrealtime();
     static_assert(XM == XM_PLAIN || MR == 1, "fused input transforms take one row");
     constexpr uint32_t E = (BITS == 4) ? 32u : 16u;  // elements per 16-byte chunk
     constexpr int XL = (BITS == 4) ? 4 : 2;          // 16-byte x loads per chunk
@@ -201,6 +209,13 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(
             sv[r][i] = buf_load_u16_aux<kSbAux>(rs, so);
             bv[r][i] = buf_load_u16_aux<kSbAux>(rb_, so);
         }
+    }
+
+    if constexpr (DIAG) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        t_land = __builtin_amdgcn_s_memrealtime();
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     if constexpr (XM != XM_PLAIN) {
@@ -324,6 +339,13 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(
 
     float tot[(RV + 3) / 4];
     wave_reduce<RV>(acc, tot);
+    if constexpr (DIAG) {
+#pragma unroll
+        for (int i = 0; i < (RV + 3) / 4; ++i) asm volatile("" ::"v"(tot[i]));
+        __builtin_amdgcn_sched_barrier(0);
+        t_math = __builtin_amdgcn_s_memrealtime();
+        __builtin_amdgcn_sched_barrier(0);
+    }
 
     // Lane 0 of each 16-lane row that holds a distinct value stores it.
     const uint32_t row16 = lane >> 4;
@@ -341,6 +363,18 @@ __global__ __launch_bounds__(256) void gemv_valu_kernel(
                     const uint32_t m = v % MR;
                     if (row < N) store_out(y, (size_t)m * N + row, tot[i], bf);
                 }
+            }
+        }
+        if constexpr (DIAG) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+            const uint64_t t_out = __builtin_amdgcn_s_memrealtime();
+            if (lane == 0) {
+                uint64_t* o = stamps + 4u * (blockIdx.x * 4u + (threadIdx.x >> 6));
+                o[0] = t_in;
+                o[1] = t_land;
+                o[2] = t_math;
+                o[3] = t_out;
             }
         }
         return;
@@ -418,6 +452,25 @@ hipError_t dispatch_mr(int mr, int rows, int cpl, const void* q, const void* s, 
 
 
 }  // namespace
+
+// Diagnostic GEMV (4-bit, M = 1, K <= 2048 so that S = 1, four rows per
+// wave): the headline kernel with per-wave wall-clock stamps. Returns the
+// number of waves through *nwaves; stamps must hold 4 * nwaves values.
+hipError_t launch_gemv_q4_timeline(const void* q, const void* s, const void* b, const void* x,
+                                   void* y, uint32_t N, uint32_t K, uint32_t G, int out_bf16,
+                                   uint64_t* stamps, uint32_t cap, uint32_t* nwaves,
+                                   hipStream_t st) {
+    uint32_t S;
+    int cpl;
+    gemv_split(4, K, &S, &cpl);
+    if (S != 1 || cpl != 1) return hipErrorInvalidValue;
+    const uint32_t grid = (N + 15u) / 16u;  // 4 rows x 4 waves per workgroup
+    *nwaves = grid * 4u;
+    if ((uint64_t)grid * 16u > cap) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemv_valu_kernel<4, 1, 4, 1, XM_PLAIN, 1>), dim3(grid), dim3(256), 0, st,
+                       q, s, b, x, y, N, K, G, S, out_bf16, (const void*)nullptr, 0.f, stamps);
+    return hipGetLastError();
+}
 
 // Split of the chunk range of a row: S K-slices over the 4 waves of a
 // workgroup, each lane taking `cpl` chunks per slice.

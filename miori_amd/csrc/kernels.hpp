@@ -12,6 +12,12 @@ hipError_t launch_gemv_valu(int bits, const void* q, const void* s, const void* 
                             const void* x, void* y, uint32_t M, uint32_t N, uint32_t K,
                             uint32_t G, int out_bf16, hipStream_t st);
 void gemv_split(int bits, uint32_t K, uint32_t* S, int* cpl);
+// The 4-bit M = 1 GEMV (K <= 2048) with per-wave wall-clock stamps (4 per
+// wave into stamps, at most cap values; *nwaves = waves launched).
+hipError_t launch_gemv_q4_timeline(const void* q, const void* s, const void* b, const void* x,
+                                   void* y, uint32_t N, uint32_t K, uint32_t G, int out_bf16,
+                                   uint64_t* stamps, uint32_t cap, uint32_t* nwaves,
+                                   hipStream_t st);
 // Fused decode ops on the 4-bit GEMV (one activation row, K <= 8192):
 // xm = 1: y = W . bf16(rmsnorm(x fp32) * w_norm bf16); xm = 2: y = W . bf16(silu(x) * x2)
 hipError_t launch_gemv_fused(int xm, const void* q, const void* s, const void* b, const void* x,

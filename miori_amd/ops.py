@@ -82,6 +82,28 @@ def gemv4(q, s, b, x, y, N, K, group=64, stream=None):
     _gemv("miori_gemv_q4", 4, q, s, b, x, y, N, K, 1, group, stream)
 
 
+def gemv4_timeline(q, s, b, x, y, N, K, group=64, stream=None):
+    """Diagnostic: gemv4 (M = 1, K <= 2048) with four wall-clock stamps per
+    wave (entry, loads landed, arithmetic done, stores complete; 100 MHz
+    s_memrealtime ticks). Returns an int64 device tensor [waves][4]; y is the
+    same as gemv4's. No counterpart in the reference."""
+    import ctypes
+
+    if K % group:
+        raise MioriError("miori_diag_gemv_q4_timeline", -2, "K must be a multiple of the group size")
+    qp, sp, bp = _qargs(q, s, b, N, K, group, 4)
+    od = _out_dtype(y)
+    xp = _ptr(x, "x", K * 2)
+    yp = _ptr(y, "y", N * y.element_size())
+    waves = (N + 15) // 16 * 4
+    st = torch.zeros((waves, 4), dtype=torch.int64, device=y.device)
+    nw = ctypes.c_uint32(0)
+    _lib.call("miori_diag_gemv_q4_timeline", qp, sp, bp, xp, yp, N, K, group, od,
+              st.data_ptr(), st.numel(), ctypes.byref(nw), _stream(stream))
+    assert nw.value == waves
+    return st
+
+
 # The reference's raw-buffer and alternative-lane-map variants compute the
 # same product (src/ops.h:105-107, 113-115, 126-128).
 gemv4_raw = gemv4

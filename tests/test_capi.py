@@ -91,3 +91,16 @@ def test_ops_rejects_host_tensors():
     q = torch.zeros(64, dtype=torch.int32)
     with pytest.raises(ValueError):
         ops.gemv4(q, q, q, q, torch.zeros(4), 4, 64)
+
+
+def test_gemv_timeline_argument_checks():
+    n = ctypes.c_uint32(0)
+    st = lambda *a: _lib.status("miori_diag_gemv_q4_timeline", *a)  # noqa: E731
+    base = (FAKE, FAKE, FAKE, FAKE, FAKE, 8192, 2048, 64, 1)
+    assert st(*base, 0, 1 << 16, ctypes.byref(n), None) == -1         # null stamps
+    assert st(*base, FAKE, 1 << 16, None, None) == -1                # null nwaves
+    assert st(FAKE, FAKE, FAKE, FAKE, FAKE, 8192, 4096, 64, 1, FAKE, 1 << 16,
+              ctypes.byref(n), None) == -2                            # K > 2048
+    assert st(*base, FAKE + 4, 1 << 16, ctypes.byref(n), None) == -3  # misaligned
+    assert st(*base, FAKE, 100, ctypes.byref(n), None) == -2          # too small
+    assert n.value == 2048                                            # 512 workgroups x 4

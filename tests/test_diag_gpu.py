@@ -69,3 +69,26 @@ def test_clock_sampler_rejects_more_than_two_seconds(dev):
     rc = _lib.status("miori_diag_clock_sample", ctypes.c_void_p(1 << 20), 1 << 20, 10**6,
                      ctypes.byref(khz), None)
     assert rc == -2
+
+
+def test_gemv_timeline_matches_gemv4(dev):
+    """The stamped diagnostic build computes the headline GEMV bit-identically
+    to miori_gemv_q4, and every wave's stamps are in order (entry <= loads
+    landed <= arithmetic done <= stores complete) and within the launch."""
+    from tests.gpu_util import acts, weights
+    N, K, G = 8192, 2048, 64
+    say(f"gemv4 timeline N={N} K={K}")
+    w, lin = weights(N, K, G, 4, seed=77, dev=dev)
+    _, xd = acts(1, K, seed=78, dev=dev)
+    y0 = torch.empty(N, dtype=torch.bfloat16, device=dev)
+    y1 = torch.empty(N, dtype=torch.bfloat16, device=dev)
+    ops.gemv4(lin.q, lin.s, lin.b, xd, y0, N, K, group=G)
+    st = ops.gemv4_timeline(lin.q, lin.s, lin.b, xd, y1, N, K, group=G)
+    torch.cuda.synchronize()
+    assert torch.equal(y0.view(torch.int16), y1.view(torch.int16))
+    s = st.cpu().numpy()
+    assert s.shape == (N // 16 * 4, 4)
+    assert np.all(s > 0)
+    assert np.all(np.diff(s, axis=1) >= 0), "stamps out of order"
+    # the whole launch spans well under a millisecond (100 MHz ticks)
+    assert s[:, 3].max() - s[:, 0].min() < 100_000
