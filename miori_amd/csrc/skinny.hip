@@ -279,8 +279,8 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
     // (their outputs are never stored; each output row depends only on its
     // own x row)
     uint32_t xro[MT];
-    // rows [m0, m0 + mstep) of y (M split over gridDim.z); x rows past that
-    // range are loaded (clamped into x) but their outputs are not stored
+    // rows [m0, m0 + mstep) of y (M split over gridDim.z); lanes of x rows
+    // past that range compute outputs that are never stored
     const uint32_t mstep = gridDim.z == 1 ? M : (M + gridDim.z - 1) / gridDim.z;
     const uint32_t m0 = blockIdx.z * mstep;
     const uint32_t m1 = min(M, m0 + mstep);
