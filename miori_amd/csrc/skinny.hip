@@ -974,6 +974,19 @@ hipError_t by_shape(uint32_t G, const void* X, const void* W, const void* S, con
                             lmh_lds_bytes(M > 16 ? 2 : 1, K, G, 8) <= 160u * 1024u &&
                             ((uintptr_t)X & 15) == 0 && e_nt < 0 && e_nw < 0;
         if (lmh_ok) {
+            // (MIORI_LMH_NWV=12 or 16, M <= 16: twelve or sixteen waves of
+            // 16 blocks in flight per workgroup instead of eight of 32, three
+            // or four waves per SIMD to hide each other's unpack and fold
+            // (116 VGPRs); a tuning experiment, off by default)
+            static const int e_lmh_nwv = tuning_env("MIORI_LMH_NWV", 8);
+            if ((e_lmh_nwv == 12 || e_lmh_nwv == 16) && M <= 16 &&
+                lmh_lds_bytes(1, K, G, e_lmh_nwv) <= 160u * 1024u) {
+                if (e_lmh_nwv == 12)
+                    return G == 64 ? launch_lmh<1, 64, 16, 12>(X, W, S, B, Y, M, N, K, out_bf16, st)
+                                   : launch_lmh<1, 128, 16, 12>(X, W, S, B, Y, M, N, K, out_bf16, st);
+                return G == 64 ? launch_lmh<1, 64, 16, 16>(X, W, S, B, Y, M, N, K, out_bf16, st)
+                               : launch_lmh<1, 128, 16, 16>(X, W, S, B, Y, M, N, K, out_bf16, st);
+            }
             // 32 blocks in flight per wave from K = 2048, else 16
             const int sel = (M > 16 ? 4 : 0) + (G == 64 ? 0 : 2) + (nbpt >= 32 ? 1 : 0);
             switch (sel) {
