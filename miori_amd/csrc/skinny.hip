@@ -297,7 +297,7 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
     // fragment read touches at one k fall on distinct banks. DMA u fills
     // tile bytes [1024u, 1024u + 1024), each lane the chunk its slot holds
     // (source row and chunk clamped into x; such slots are never read). The
-    // DMAs are issued before the first block so its wait covers them.
+    // wait for the first block covers the DMAs (issue order below).
     typedef __attribute__((address_space(3))) const u32x4_t* lds_v4;
     const uint32_t xrows = min(16u * MT, m1 - m0);
     const uint32_t kbase = kb0 * C::KB;
@@ -309,7 +309,9 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
         xrb[mt] = __umul24(row, rsb);
         xsw[mt] = row & 15u;
     }
-    if constexpr (C::XL) {
+    // (issued after block 0's weight loads, below)
+    auto issue_xtile = [&]() {
+      if constexpr (C::XL) {
         const uint32_t nins = (xrows * rsb + 1023u) / 1024u;
         const uint32_t nch = nloc * C::KB / 8u;
         // xrot != 0: the workgroups of one XCD (blockIdx.x % 8 alike) start
@@ -336,7 +338,8 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
             const uint32_t ch = min(((p - __umul24(r, rsb)) >> 4) ^ (r & 15u), nch - 1u);
             dma16(X + (xoff0 + __umul24(rr, K) + ch * 8u), xdyn + u * 1024u);
         }
-    }
+      }
+    };
 
     // block slots
     u32x4_t wr[C::DEPTH][NT][C::WL];
@@ -537,9 +540,15 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
         if constexpr (i + C::DEPTH < NBW) issue(blk_of(i + C::DEPTH), ic<sl>{});
         __builtin_amdgcn_sched_barrier(0);
     };
+    // Issue order: block 0's loads, then the x tile's DMAs, then the scale /
+    // bias tiles' DMAs, then blocks 1 .. DEPTH-1. The wait of block 0 keeps
+    // only the DEPTH-1 youngest blocks in flight, so it covers both DMA sets;
+    // block 0's weights (from HBM) go out first and their latency overlaps
+    // the DMA issue (the x tile mostly comes from L2).
+    issue(blk_of(0), ic<0>{});
+    issue_xtile();
     // Scale / bias tiles of rows n0 .. n0+NB-1 (contiguous in S and B): 1 KiB
-    // DMA chunks spread over the waves, issued before the first block so the
-    // wait for block 0 covers them. Sources are clamped inside the arrays.
+    // DMA chunks spread over the waves. Sources are clamped inside the arrays.
     if constexpr (MODE != BF16) {
         const uint32_t tb = C::NB * ng * 2u;                 // tile bytes
         const size_t total = (size_t)N * ng * 2u;            // array bytes
@@ -550,7 +559,6 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
             dma16(reinterpret_cast<const uint8_t*>(Bi) + off, lds + C::SB_BYTES + q * 1024u);
         }
     }
-    issue(blk_of(0), ic<0>{});
     if constexpr (C::DEPTH > 1) issue(blk_of(1), ic<1 % C::DEPTH>{});
     if constexpr (C::DEPTH > 2) issue(blk_of(2), ic<2 % C::DEPTH>{});
     if constexpr (C::DEPTH > 3) issue(blk_of(3), ic<3 % C::DEPTH>{});
