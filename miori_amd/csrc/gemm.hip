@@ -769,7 +769,9 @@ __global__ __launch_bounds__(512) void gemm_pc_kernel(
 template <int BM>
 struct CfgQ {  // wave tile of the fused register-B form, for the epilogue
     static constexpr int WM = BM, WN = 32, TM = BM / 32, TN = 1;
-    static constexpr int EPR = 128;  // 4 waves x 128 rows x 40 floats fit the A ring
+    // rows per epilogue pass: 4 waves x 128 (or 64) rows x 40 floats fit the
+    // A ring
+    static constexpr int EPR = BM % 128 == 0 ? 128 : 64;
 };
 
 template <int BM, int BN, int G>
@@ -1257,6 +1259,39 @@ hipError_t launch_tile(const void* A, const void* B, const void* q, const void* 
     return hipErrorInvalidValue;
 }
 
+// Fused 4-bit GEMM on 192x128 tiles (gemm_pcq_kernel, unsplit).
+hipError_t launch_fused_192(const void* A, const void* q, const void* s, const void* b, void* C,
+                            uint32_t M, uint32_t N, uint32_t K, uint32_t G, int out_bf16,
+                            hipStream_t st) {
+    constexpr int BM = 192, BN = 128;
+    const uint32_t tiles_m = (M + BM - 1) / BM;
+    const uint32_t ntiles = tiles_m * ((N + BN - 1) / BN);
+    static const int remap = tuning_env("MIORI_GEMM_REMAP", 1);
+    switch (G) {
+        case 32:
+            hipLaunchKernelGGL((gemm_pcq_kernel<BM, BN, 32>), dim3(ntiles), dim3(512), 0, st,
+                               (const uint16_t*)A, (const uint32_t*)q, (const uint16_t*)s,
+                               (const uint16_t*)b, C, M, N, K, out_bf16, tiles_m, remap, nullptr,
+                               1u, ntiles);
+            break;
+        case 64:
+            hipLaunchKernelGGL((gemm_pcq_kernel<BM, BN, 64>), dim3(ntiles), dim3(512), 0, st,
+                               (const uint16_t*)A, (const uint32_t*)q, (const uint16_t*)s,
+                               (const uint16_t*)b, C, M, N, K, out_bf16, tiles_m, remap, nullptr,
+                               1u, ntiles);
+            break;
+        case 128:
+            hipLaunchKernelGGL((gemm_pcq_kernel<BM, BN, 128>), dim3(ntiles), dim3(512), 0, st,
+                               (const uint16_t*)A, (const uint32_t*)q, (const uint16_t*)s,
+                               (const uint16_t*)b, C, M, N, K, out_bf16, tiles_m, remap, nullptr,
+                               1u, ntiles);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 // K splits for `tiles` BM x BN output tiles of KT K tiles each, one
 // workgroup per CU at a time. Cost in half-K-tile units (a 64-deep K tile of
 // a 128x128 workgroup takes ~0.6 us): rounds of 256 workgroups x K tiles per
@@ -1298,7 +1333,7 @@ hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* 
                        uint32_t G, int out_bf16, hipStream_t st) {
     // Tile choice (MIORI_GEMM_TILE overrides: 0 = 256x128, 1 = 128x128,
     // 2 = 256x256, 3 = 64x128, 4 = 64x64, 5 = 192x256, 6 = 128x128 split as
-    // the 64x128 grid):
+    // the 64x128 grid, 7 = 192x128 fused):
     //  * bf16 weight cache: 256x256 tiles (128 flop per operand byte, against
     //    85 for 256x128) once they fill at least 3/4 of the 256 CUs in a
     //    round; the split-K cost model is not applied to them (SK = 1).
@@ -1336,7 +1371,19 @@ hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* 
     if (tile == 5 && !q && e_w8) return launch_w8<192, 256>(A, B, C, M, N, K, out_bf16, st);
     if (tile == 2 && !q) return launch_cfg<256, 256, false, 64>(A, B, q, s, b, C, M, N, K, out_bf16, 1, st);
     if (tile == 5 && !q) return launch_cfg<192, 256, false, 64>(A, B, q, s, b, C, M, N, K, out_bf16, 1, st);
-    if (tile == 2 || tile == 5) tile = pick_tile_256x128(M, N, K);  // fused: no 256x256 variant
+    if (tile == 5 && q && e_tile < 0) {
+        // Fused 4-bit where the bf16 path takes 192x256 tiles (M=1472,
+        // N=8192): 192x128 tiles when their grid's rounds cost less than
+        // 256x128 ones, a round of 192-row tiles taking about 3/4 of a
+        // 256-row one. M=1472, N=8192: 8 x 64 = 512 tiles in two full rounds
+        // (2 x 3/4) against 6 x 64 = 384 256x128 tiles in two rounds, the
+        // second half empty (2 x 1). Unsplit, like the bf16 tall tiles.
+        const uint64_t t192 = (uint64_t)((M + 191) / 192) * ((N + 127) / 128);
+        const uint64_t t256 = (uint64_t)((M + 255) / 256) * ((N + 127) / 128);
+        if ((t192 + 255) / 256 * 3 < (t256 + 255) / 256 * 4) tile = 7;
+    }
+    if (tile == 7 && q) return launch_fused_192(A, q, s, b, C, M, N, K, G, out_bf16, st);
+    if (tile == 2 || tile == 5 || tile == 7) tile = pick_tile_256x128(M, N, K);  // fused: no 256x256 variant
     // (64x64, and the fused path's 128x128 tiles on these small grids, split
     // as the 64x128 grid)
     const uint32_t tbm = tile == 0 ? 256 : (tile == 3 || tile == 4 || tile == 6) ? 64 : 128;

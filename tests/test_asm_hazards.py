@@ -112,7 +112,7 @@ def test_gemm_kernel_waits(tmp_path):
     assert not bad, {k[:80]: v[:3] for k, v in bad.items()}
     assert not _spilled(text, "gemm_w8_kernel")
     res = check_file(text, "gemm_pcq_kernel")
-    assert len(res) == 6, "expected every gemm_pcq_kernel instantiation"
+    assert len(res) == 9, "expected every gemm_pcq_kernel instantiation"
     bad = {k: v for k, v in res.items() if v}
     assert not bad, {k[:80]: v[:3] for k, v in bad.items()}
     assert not _spilled(text, "gemm_pcq_kernel")
