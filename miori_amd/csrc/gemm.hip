@@ -1259,39 +1259,6 @@ hipError_t launch_tile(const void* A, const void* B, const void* q, const void* 
     return hipErrorInvalidValue;
 }
 
-// Fused 4-bit GEMM on 192x128 tiles (gemm_pcq_kernel, unsplit).
-hipError_t launch_fused_192(const void* A, const void* q, const void* s, const void* b, void* C,
-                            uint32_t M, uint32_t N, uint32_t K, uint32_t G, int out_bf16,
-                            hipStream_t st) {
-    constexpr int BM = 192, BN = 128;
-    const uint32_t tiles_m = (M + BM - 1) / BM;
-    const uint32_t ntiles = tiles_m * ((N + BN - 1) / BN);
-    static const int remap = tuning_env("MIORI_GEMM_REMAP", 1);
-    switch (G) {
-        case 32:
-            hipLaunchKernelGGL((gemm_pcq_kernel<BM, BN, 32>), dim3(ntiles), dim3(512), 0, st,
-                               (const uint16_t*)A, (const uint32_t*)q, (const uint16_t*)s,
-                               (const uint16_t*)b, C, M, N, K, out_bf16, tiles_m, remap, nullptr,
-                               1u, ntiles);
-            break;
-        case 64:
-            hipLaunchKernelGGL((gemm_pcq_kernel<BM, BN, 64>), dim3(ntiles), dim3(512), 0, st,
-                               (const uint16_t*)A, (const uint32_t*)q, (const uint16_t*)s,
-                               (const uint16_t*)b, C, M, N, K, out_bf16, tiles_m, remap, nullptr,
-                               1u, ntiles);
-            break;
-        case 128:
-            hipLaunchKernelGGL((gemm_pcq_kernel<BM, BN, 128>), dim3(ntiles), dim3(512), 0, st,
-                               (const uint16_t*)A, (const uint32_t*)q, (const uint16_t*)s,
-                               (const uint16_t*)b, C, M, N, K, out_bf16, tiles_m, remap, nullptr,
-                               1u, ntiles);
-            break;
-        default:
-            return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
-}
-
 // K splits for `tiles` BM x BN output tiles of KT K tiles each, one
 // workgroup per CU at a time. Cost in half-K-tile units (a 64-deep K tile of
 // a 128x128 workgroup takes ~0.6 us): rounds of 256 workgroups x K tiles per
@@ -1317,12 +1284,19 @@ uint32_t pick_split(uint32_t tiles, uint32_t KT, uint64_t MN, uint64_t* cost_out
 // 128x128 one (fused 4-bit: 56 us per 256x128 round at M=1024, N=8192, K=2048;
 // 37 us per 128x128 round at M=1472). A function of the tile grids and K
 // only, so the fused and the bf16 products of one shape pick alike.
+// 192x128 tiles (tile 7) compete at 24/20, between the two: M=1472, K=8192,
+// N=2048 then runs 8 x 16 = 128 tiles split in two, one full round of 256
+// workgroups, instead of 96 256x128 tiles split in two on 192 CUs.
 int pick_tile_256x128(uint32_t M, uint32_t N, uint32_t K) {
     const uint32_t t0 = ((M + 255) / 256) * ((N + 127) / 128);
     const uint32_t t1 = ((M + 127) / 128) * ((N + 127) / 128);
-    uint64_t c0 = 0, c1 = 0;
+    const uint32_t t7 = ((M + 191) / 192) * ((N + 127) / 128);
+    uint64_t c0 = 0, c1 = 0, c7 = 0;
     pick_split(t0, K / 64, (uint64_t)t0 * 256 * 128, &c0);
     pick_split(t1, K / 64, (uint64_t)t1 * 128 * 128, &c1);
+    pick_split(t7, K / 64, (uint64_t)t7 * 192 * 128, &c7);
+    static const int e_192 = tuning_env("MIORI_GEMM_192", 1);
+    if (e_192 && c7 * 24 < c0 * 27 && c7 * 24 < c1 * 20) return 7;
     return c0 * 27 <= c1 * 20 ? 0 : 1;
 }
 
@@ -1371,6 +1345,7 @@ hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* 
     if (tile == 5 && !q && e_w8) return launch_w8<192, 256>(A, B, C, M, N, K, out_bf16, st);
     if (tile == 2 && !q) return launch_cfg<256, 256, false, 64>(A, B, q, s, b, C, M, N, K, out_bf16, 1, st);
     if (tile == 5 && !q) return launch_cfg<192, 256, false, 64>(A, B, q, s, b, C, M, N, K, out_bf16, 1, st);
+    const bool t5 = tile == 5;  // the bf16 path's 192x256 choice (fused: 192x128, unsplit)
     if (tile == 5 && q && e_tile < 0) {
         // Fused 4-bit where the bf16 path takes 192x256 tiles (M=1472,
         // N=8192): 192x128 tiles when their grid's rounds cost less than
@@ -1382,11 +1357,11 @@ hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* 
         const uint64_t t256 = (uint64_t)((M + 255) / 256) * ((N + 127) / 128);
         if ((t192 + 255) / 256 * 3 < (t256 + 255) / 256 * 4) tile = 7;
     }
-    if (tile == 7 && q) return launch_fused_192(A, q, s, b, C, M, N, K, G, out_bf16, st);
-    if (tile == 2 || tile == 5 || tile == 7) tile = pick_tile_256x128(M, N, K);  // fused: no 256x256 variant
+    if (tile == 7 && q && t5) return launch_tile<192, 128>(A, B, q, s, b, C, M, N, K, G, out_bf16, 1, st);
+    if (tile == 2 || tile == 5) tile = pick_tile_256x128(M, N, K);  // fused: no 256x256 variant
     // (64x64, and the fused path's 128x128 tiles on these small grids, split
     // as the 64x128 grid)
-    const uint32_t tbm = tile == 0 ? 256 : (tile == 3 || tile == 4 || tile == 6) ? 64 : 128;
+    const uint32_t tbm = tile == 0 ? 256 : tile == 7 ? 192 : (tile == 3 || tile == 4 || tile == 6) ? 64 : 128;
     const uint32_t tbn = 128;
     const uint32_t ntiles = ((M + tbm - 1) / tbm) * ((N + tbn - 1) / tbn);
     // partial traffic from the padded tile grid, so every M in one row-tile
@@ -1399,6 +1374,7 @@ hipError_t launch_gemm(const void* A, const void* B, const void* q, const void* 
     if (SK > 16) SK = 16;
     if (SK > K / 64) SK = K / 64;
     if (tile == 0) return launch_tile<256, 128>(A, B, q, s, b, C, M, N, K, G, out_bf16, SK, st);
+    if (tile == 7) return launch_tile<192, 128>(A, B, q, s, b, C, M, N, K, G, out_bf16, SK, st);
     if (tile == 3) return launch_tile<64, 128>(A, B, q, s, b, C, M, N, K, G, out_bf16, SK, st);
     if (tile == 4 && !q) return launch_cfg<64, 64, false, 64>(A, B, q, s, b, C, M, N, K, out_bf16, SK, st);
     return launch_tile<128, 128>(A, B, q, s, b, C, M, N, K, G, out_bf16, SK, st);

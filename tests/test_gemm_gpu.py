@@ -157,7 +157,8 @@ np.save(sys.argv[7], C.cpu().numpy())
 """
 
 
-@pytest.mark.parametrize("M,K,N", [(1024, 2048, 8192), (1472, 2048, 2560), (300, 8192, 2048)])
+@pytest.mark.parametrize("M,K,N", [(1024, 2048, 8192), (1472, 2048, 2560), (300, 8192, 2048),
+                                   (1472, 8192, 2048)])  # the last on 192x128 tiles, split in 2
 def test_gemm_producer_consumer_matches_classic(dev, tmp_path, M, K, N):
     """The eight-wave producer/consumer bf16 GEMM (the default for 256x128
     and 128x128 tiles, 16x16x32 MFMAs) agrees with the four-wave form on the

@@ -84,7 +84,7 @@ def test_eight_wave_maps(BM, BN):
     assert 8 * 32 * (WN + 8) * 4 <= 2 * (A_ST + B_ST)
 
 
-@pytest.mark.parametrize("BM,BN", [(256, 128), (128, 128)])
+@pytest.mark.parametrize("BM,BN", [(256, 128), (192, 128), (128, 128)])
 def test_producer_consumer_maps(BM, BN):
     WM, WN = BM // 2, BN // 2
     A_ST, B_ST = BM * ROWB, BN * ROWB
@@ -156,7 +156,7 @@ def test_skinny_x_tile_map(KB, nloc, xrows):
             assert len(banks) == 16
 
 
-@pytest.mark.parametrize("rows,nfrag", [(256, 8), (128, 4), (64, 2)])
+@pytest.mark.parametrize("rows,nfrag", [(256, 8), (192, 6), (128, 4), (64, 2)])
 def test_mfma32_fragment_map(rows, nfrag):
     """The 32x32x16 fragment reads of gemm_kernel and gemm_pcq_kernel: in
     k-step ks (four per 64-deep K tile) lane half h = lane / 32 reads chunk
