@@ -770,7 +770,7 @@ template <int BM>
 struct CfgQ {  // wave tile of the fused register-B form, for the epilogue
     static constexpr int WM = BM, WN = 32, TM = BM / 32, TN = 1;
     // rows per epilogue pass: 4 waves x 128 (or 64) rows x 40 floats fit the
-    // A ring
+    // kernel's LDS (checked in the kernel)
     static constexpr int EPR = BM % 128 == 0 ? 128 : 64;
 };
 

@@ -226,3 +226,39 @@ def test_fp32_row_division_exhaustive():
         inv = np.float32(1.0) / np.float32(d)
         q = ((a.astype(np.float32) + np.float32(0.5)) * inv).astype(np.int64)
         assert np.array_equal(q, a // d), d
+
+
+@pytest.mark.parametrize("BM,EPR", [(256, 128), (192, 64), (128, 128)])
+def test_fused_epilogue_passes_cover_the_wave_tile(BM, EPR):
+    """gemm_pcq_kernel's epilogue (gemm.hip store_wave_tile / store_wave_rows
+    with the fused form's wave tile, BM rows x 32 columns of 32x32 MFMA
+    tiles): pass ps stages MFMA tiles [ps*EPR/32, (ps+1)*EPR/32) into rows
+    (i - ps*EPR/32)*32 + 8*(e/4) + 4*(lane/32) + e%4 of an EPR x (32 + 8)
+    fp32 region, column lane % 32; the read-back stores row ps*EPR + r.
+    Every element of the BM x 32 tile is staged once and lands on its own
+    output row and column; the four waves' regions fit the kernel's LDS
+    (three stages of BM x 128 bytes of A and of 128 x 128 bytes)."""
+    WN, RS = 32, 40
+    TM = BM // 32
+    assert BM % EPR == 0 and EPR % 32 == 0
+    assert 4 * EPR * RS * 4 <= 3 * BM * 128 + 3 * 128 * 128
+    seen = {}
+    for ps in range(BM // EPR):
+        region = {}
+        for i in range(TM):
+            if i < ps * (EPR // 32) or i >= (ps + 1) * (EPR // 32):
+                continue
+            for lane in range(64):
+                for e in range(16):
+                    r = (i - ps * (EPR // 32)) * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)
+                    assert 0 <= r < EPR
+                    key = (r, lane & 31)
+                    assert key not in region
+                    # the MFMA element's true position in the wave tile
+                    region[key] = (32 * i + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3), lane & 31)
+        for (r, c), src in region.items():
+            out = (ps * EPR + r, c)
+            assert out == src
+            assert out not in seen
+            seen[out] = True
+    assert len(seen) == BM * WN
