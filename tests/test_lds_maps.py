@@ -262,3 +262,35 @@ def test_fused_epilogue_passes_cover_the_wave_tile(BM, EPR):
             assert out not in seen
             seen[out] = True
     assert len(seen) == BM * WN
+
+
+@pytest.mark.parametrize("BM,BN", [(256, 128), (192, 128), (128, 128)])
+def test_producer_consumer_epilogue_covers_the_wave_tile(BM, BN):
+    """gemm_pc_kernel's epilogue (store_wave_tile16): each consumer wave's
+    (BM/2) x (BN/2) tile of 16x16 MFMA tiles is staged EPR rows per pass
+    (EPR = BM/2 when the four waves' regions of EPR x (BN/2 + 8) floats fit
+    the kernel's LDS, else 32), element e of lane l of tile (i, j) at row
+    (i - ps*EPR/16)*16 + 4*(l/16) + e, column 16j + l%16, and read back as
+    row ps*EPR + r. Every element lands once, on its own row and column."""
+    WM, WN = BM // 2, BN // 2
+    RS = WN + 8
+    lds = 3 * BM * 128 + 3 * BN * 128
+    EPR = WM if 4 * WM * RS * 4 <= lds else 32
+    assert WM % EPR == 0 and EPR % 32 == 0
+    seen = set()
+    for ps in range(WM // EPR):
+        region = {}
+        for i in range(WM // 16):
+            if i < ps * (EPR // 16) or i >= (ps + 1) * (EPR // 16):
+                continue
+            for j in range(WN // 16):
+                for lane in range(64):
+                    for e in range(4):
+                        r = (i - ps * (EPR // 16)) * 16 + 4 * (lane >> 4) + e
+                        c = j * 16 + (lane & 15)
+                        assert 0 <= r < EPR and (r, c) not in region
+                        region[(r, c)] = (16 * i + 4 * (lane >> 4) + e, c)
+        for (r, c), src in region.items():
+            assert (ps * EPR + r, c) == src and src not in seen
+            seen.add(src)
+    assert len(seen) == WM * WN
