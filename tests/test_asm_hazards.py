@@ -147,3 +147,18 @@ def test_skinny_kernel_waits(tmp_path):
     bad = {k: v for k, v in res.items() if v}
     assert not bad, {k[:80]: v[:3] for k, v in bad.items()}
     assert not [n for n, sz in scratch if "lmh_kernel" in n and int(sz) > 0]
+
+
+@pytest.mark.skipif(not shutil.which(HIPCC) and not os.path.exists(HIPCC), reason="hipcc not available")
+def test_gemv_kernel_waits(tmp_path):
+    """The GEMV kernels use compiler-placed waits, plus one hand-placed full
+    wait in the stamped diagnostic build (miori_diag_gemv_q4_timeline): the
+    checker finds no early use in any instantiation, the diagnostic one
+    included, and nothing spills."""
+    text = _compile("gemv.hip", tmp_path / "gemv.s")
+    res = check_file(text, "gemv_valu_kernel")
+    assert len(res) >= 40, "expected every gemv_valu_kernel instantiation"
+    assert any("ELi1EEEv" in k for k in res), "the diagnostic instantiation"
+    bad = {k: v for k, v in res.items() if v}
+    assert not bad, {k[:80]: v[:3] for k, v in bad.items()}
+    assert not _spilled(text, "gemv_valu_kernel")
