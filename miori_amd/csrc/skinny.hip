@@ -622,7 +622,13 @@ __global__ __launch_bounds__(NWV * 64) void skinny_kernel(
 //    loads from 16 rows, took 93 us at M = 32.)
 //  * Requires G in {64, 128}, K / 64 a power of two >= DEPTH, and the x tile
 //    (16*MT rows of 2K bytes) plus the scale buffers within 160 KiB.
-template <int MT, int G, int DEPTH, int NWV>
+//
+// XS = true (MIORI_LMH_XSUM=1, a tuning experiment): the x sums X_g of each
+// 64-k block and m-tile, which do not depend on the weight rows, are made
+// once per workgroup into LDS (the same two MFMAs against ones as the
+// per-block code, so the products stay bit-identical) and each block reads
+// them instead of recomputing them: half the MFMAs per block.
+template <int MT, int G, int DEPTH, int NWV, bool XS = false>
 __global__ __launch_bounds__(NWV * 64) void lmh_kernel(const uint16_t* __restrict__ X,
                                                   const uint8_t* __restrict__ W,
                                                   const uint16_t* __restrict__ S,
@@ -678,6 +684,31 @@ __global__ __launch_bounds__(NWV * 64) void lmh_kernel(const uint16_t* __restric
     if (T > 0) issue_sb(0);
     wait_vm<0>();
     barrier_lds();
+    // (XS) x sums after the scale buffers: [block][m-tile][quarter c] x 4
+    // floats, rows 4c + e of the m-tile; the MFMA against ones gives every
+    // column the same sums, so lane 16c stores them.
+    uint8_t* const xsum = xs + 16u * MT * XR + NWV * (4u * sbc * 1024u);
+    if constexpr (XS) {
+        typedef __attribute__((address_space(3))) const u32x4_t* lds_v4x;
+        const bf16x8_t ones1 = as_bf16x8_u(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+        for (uint32_t kb = wave; kb < nbpt; kb += NWV) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const uint32_t r = min(mt * 16u + j, rows - 1u), sw = r & 15u;
+                const uint32_t base = (kb & ~1u) * (KB * 2u) + r * XR;
+                bf16x8_t f[2];
+#pragma unroll
+                for (int q = 0; q < 2; ++q)
+                    f[q] = __builtin_bit_cast(
+                        bf16x8_t, *(lds_v4x)(xs + base + ((((kb & 1u) * 8u + kmap<Q8X, G>(c, q) / 8u) ^ sw) << 4)));
+                f32x4_t dx = mfma16(f[0], ones1, f32x4_t{0.f, 0.f, 0.f, 0.f});
+                dx = mfma16(f[1], ones1, dx);
+                if ((lane & 15u) == 0)
+                    *reinterpret_cast<f32x4_t*>(xsum + ((kb * MT + mt) * 4u + c) * 16u) = dx;
+            }
+        }
+        barrier_lds();
+    }
     if (T == 0) return;
 
     u32x4_t wr[DEPTH];
@@ -720,7 +751,8 @@ __global__ __launch_bounds__(NWV * 64) void lmh_kernel(const uint16_t* __restric
 
     // block i of the chunk: xc = x tile + kb0 * 128 bytes, sc_b / bi_b = this
     // lane's scale / bias row at the chunk's first group
-    auto compute = [&](const uint8_t* xc, lds_u16 sc_b, lds_u16 bi_b, auto i_c) {
+    auto compute = [&](const uint8_t* xc, lds_u16 sc_b, lds_u16 bi_b, const uint8_t* xsc,
+                       auto i_c) {
         constexpr int i = decltype(i_c)::value;
         bf16x8_t xf[MT][2];
 #pragma unroll
@@ -736,8 +768,13 @@ __global__ __launch_bounds__(NWV * 64) void lmh_kernel(const uint16_t* __restric
         const bf16x8_t q0 = codes8_bf16(w0, w1), q1 = codes8_bf16(w2, w3);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-            f32x4_t dx = mfma16(xf[mt][0], ones, f32x4_t{0.f, 0.f, 0.f, 0.f});
-            dx = mfma16(xf[mt][1], ones, dx);
+            f32x4_t dx;
+            if constexpr (XS) {
+                dx = *(const __attribute__((address_space(3))) f32x4_t*)(xsc + ((i * MT + mt) * 4 + c) * 16u);
+            } else {
+                dx = mfma16(xf[mt][0], ones, f32x4_t{0.f, 0.f, 0.f, 0.f});
+                dx = mfma16(xf[mt][1], ones, dx);
+            }
             f32x4_t dd = mfma16(xf[mt][0], q0, f32x4_t{0.f, 0.f, 0.f, 0.f});
             dd = mfma16(xf[mt][1], q1, dd);
 #pragma unroll
@@ -752,6 +789,7 @@ __global__ __launch_bounds__(NWV * 64) void lmh_kernel(const uint16_t* __restric
     for (uint32_t b0 = 0; b0 < total; b0 += DEPTH) {
         const uint32_t kb0 = b0 & (nbpt - 1u), bn = b0 + DEPTH;
         const uint8_t* xc = xs + kb0 * (KB * 2u);
+        const uint8_t* xsc = xsum + kb0 * (MT * 64u);
         const uint8_t* sbb = sbw + ((b0 >> lg) & 1u) * (2u * sbc * 1024u);
         const lds_u16 sc_b = (lds_u16)sbb + j * ng + kb0 * KB / G;
         const lds_u16 bi_b = (lds_u16)(sbb + sbc * 1024u) + j * ng + kb0 * KB / G;
@@ -767,7 +805,7 @@ __global__ __launch_bounds__(NWV * 64) void lmh_kernel(const uint16_t* __restric
             wait_vm<DEPTH - 1>();
             tie(wr[i]);
             __builtin_amdgcn_sched_barrier(0);
-            compute(xc, sc_b, bi_b, i_c);
+            compute(xc, sc_b, bi_b, xsc, i_c);
             if constexpr (i == 0)
                 if ((bn & (nbpt - 1u)) == 0 && (bn >> lg) < T) issue_sb(bn >> lg);
             issue(nb, i_c);
@@ -793,12 +831,13 @@ __global__ __launch_bounds__(NWV * 64) void lmh_kernel(const uint16_t* __restric
 }
 
 // x tile plus the waves' double-buffered scale / bias tiles
-inline size_t lmh_lds_bytes(int mt, uint32_t K, uint32_t G, int nwv) {
+inline size_t lmh_lds_bytes(int mt, uint32_t K, uint32_t G, int nwv, bool xsum = false) {
     const size_t sbc = (32u * (K / G) + 1023u) / 1024u;
-    return (size_t)16 * mt * 2u * K + (size_t)nwv * 4 * sbc * 1024;
+    return (size_t)16 * mt * 2u * K + (size_t)nwv * 4 * sbc * 1024 +
+           (xsum ? (size_t)(K / 64) * mt * 64 : 0);
 }
 
-template <int MT, int G, int DEPTH, int NWV>
+template <int MT, int G, int DEPTH, int NWV, bool XS = false>
 hipError_t launch_lmh(const void* X, const void* W, const void* S, const void* B, void* Y,
                       uint32_t M, uint32_t N, uint32_t K, int out_bf16, hipStream_t st) {
     // CU count of each device, and (dynamic LDS above 64 KiB is opted into
@@ -813,18 +852,18 @@ hipError_t launch_lmh(const void* X, const void* W, const void* S, const void* B
         hipError_t r = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
         if (r != hipSuccess) return r;
         if (n <= 0) return hipErrorInvalidDevice;
-        r = hipFuncSetAttribute((const void*)lmh_kernel<MT, G, DEPTH, NWV>,
+        r = hipFuncSetAttribute((const void*)lmh_kernel<MT, G, DEPTH, NWV, XS>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (r == hipSuccess) cus[dev].store(n, std::memory_order_relaxed);
         return r;
     });
     if (e != hipSuccess) return e;
-    const size_t lds = lmh_lds_bytes(MT, K, G, NWV);
+    const size_t lds = lmh_lds_bytes(MT, K, G, NWV, XS);
     static const uint32_t xrot = (uint32_t)tuning_env("MIORI_SKINNY_XROT", 0);
     const uint32_t ntiles = (N + 15u) / 16u;
     const uint32_t grid = std::min<uint32_t>((uint32_t)cus[dev].load(std::memory_order_relaxed),
                                              (ntiles + NWV - 1u) / NWV);
-    hipLaunchKernelGGL((lmh_kernel<MT, G, DEPTH, NWV>), dim3(grid), dim3(NWV * 64), lds, st,
+    hipLaunchKernelGGL((lmh_kernel<MT, G, DEPTH, NWV, XS>), dim3(grid), dim3(NWV * 64), lds, st,
                        (const uint16_t*)X, (const uint8_t*)W, (const uint16_t*)S,
                        (const uint16_t*)B, Y, M, N, K, out_bf16, xrot);
     return hipGetLastError();
@@ -997,6 +1036,20 @@ hipError_t by_shape(uint32_t G, const void* X, const void* W, const void* S, con
             }
             // 32 blocks in flight per wave from K = 2048, else 16
             const int sel = (M > 16 ? 4 : 0) + (G == 64 ? 0 : 2) + (nbpt >= 32 ? 1 : 0);
+            // (MIORI_LMH_XSUM=1: x sums made once per workgroup, an experiment)
+            static const int e_xs = tuning_env("MIORI_LMH_XSUM", 0);
+            if (e_xs && lmh_lds_bytes(M > 16 ? 2 : 1, K, G, 8, true) <= 160u * 1024u) {
+                switch (sel) {
+                    case 0: return launch_lmh<1, 64, 16, 8, true>(X, W, S, B, Y, M, N, K, out_bf16, st);
+                    case 1: return launch_lmh<1, 64, 32, 8, true>(X, W, S, B, Y, M, N, K, out_bf16, st);
+                    case 2: return launch_lmh<1, 128, 16, 8, true>(X, W, S, B, Y, M, N, K, out_bf16, st);
+                    case 3: return launch_lmh<1, 128, 32, 8, true>(X, W, S, B, Y, M, N, K, out_bf16, st);
+                    case 4: return launch_lmh<2, 64, 16, 8, true>(X, W, S, B, Y, M, N, K, out_bf16, st);
+                    case 5: return launch_lmh<2, 64, 32, 8, true>(X, W, S, B, Y, M, N, K, out_bf16, st);
+                    case 6: return launch_lmh<2, 128, 16, 8, true>(X, W, S, B, Y, M, N, K, out_bf16, st);
+                    default: return launch_lmh<2, 128, 32, 8, true>(X, W, S, B, Y, M, N, K, out_bf16, st);
+                }
+            }
             switch (sel) {
                 case 0: return launch_lmh<1, 64, 16, 8>(X, W, S, B, Y, M, N, K, out_bf16, st);
                 case 1: return launch_lmh<1, 64, 32, 8>(X, W, S, B, Y, M, N, K, out_bf16, st);

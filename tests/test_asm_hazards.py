@@ -141,9 +141,9 @@ def test_skinny_kernel_waits(tmp_path):
     spilled = [n for n, sz in scratch if "skinny_kernel" in n and int(sz) > 0]
     assert names and not spilled, spilled[:5]
     # the persistent 8-bit form (M tiles x group x depth, eight waves; and
-    # the twelve- and sixteen-wave experiments)
+    # the twelve- and sixteen-wave and x-sum experiments)
     res = check_file(text, "lmh_kernel")
-    assert len(res) == 12, "expected every lmh_kernel instantiation"
+    assert len(res) == 20, "expected every lmh_kernel instantiation"
     bad = {k: v for k, v in res.items() if v}
     assert not bad, {k[:80]: v[:3] for k, v in bad.items()}
     assert not [n for n, sz in scratch if "lmh_kernel" in n and int(sz) > 0]

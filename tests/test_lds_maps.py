@@ -294,3 +294,23 @@ def test_producer_consumer_epilogue_covers_the_wave_tile(BM, BN):
             assert (ps * EPR + r, c) == src and src not in seen
             seen.add(src)
     assert len(seen) == WM * WN
+
+
+@pytest.mark.parametrize("depth,nbpt", [(16, 16), (16, 32), (32, 32), (32, 64)])
+def test_lm_head_xsum_reads_the_block_fragments(depth, nbpt):
+    """MIORI_LMH_XSUM: the x sums of block kb are made from the x-tile bytes
+    at (kb & ~1) * 128 + xa[kb & 1] (xa the per-lane row and swizzled chunk
+    offset), while the per-block code reads block i of the chunk starting
+    at kb0 (a multiple of DEPTH) at kb0 * 128 + (i / 2) * 256 + xa[i % 2]:
+    the same bytes for every kb; and the sums' slots ((kb * MT + mt) * 4 + c)
+    * 16 bytes, read at xsum + kb0 * MT * 64 + ((i * MT + mt) * 4 + c) * 16,
+    agree too."""
+    for MT in (1, 2):
+        for kb0 in range(0, nbpt, depth):
+            for i in range(depth):
+                kb = kb0 + i
+                assert kb0 * 128 + (i // 2) * 256 == (kb & ~1) * 128 and i % 2 == kb & 1
+                for mt in range(MT):
+                    for c in range(4):
+                        assert (kb0 * MT * 64 + ((i * MT + mt) * 4 + c) * 16
+                                == ((kb * MT + mt) * 4 + c) * 16)

@@ -1,10 +1,12 @@
 """The tuning experiments behind environment switches compute the same
 products as the defaults, bit for bit: MIORI_LMH_NWV=12/16 (the persistent
-8-bit kernel with twelve or sixteen waves of 16 blocks in flight) and
+8-bit kernel with twelve or sixteen waves of 16 blocks in flight),
 MIORI_SKINNY_XROT=1 (rotated x-tile DMA order in the skinny and persistent
-kernels). Neither changes any output's arithmetic or its order: a tile's
-blocks are folded in k order by one wave whatever the wave count and depth,
-and the x tile holds the same bytes whatever order its DMAs run in.
+kernels) and MIORI_LMH_XSUM=1 (the persistent kernel's x sums made once per
+workgroup by the same MFMAs). None changes any output's arithmetic or its
+order: a tile's blocks are folded in k order by one wave whatever the wave
+count and depth, the x tile holds the same bytes whatever order its DMAs run
+in, and each x sum is the same MFMA on the same fragments.
 
 The switches are read once per process, so each variant runs in a child
 process; the parent computes the default products and compares."""
@@ -58,7 +60,7 @@ def run_cases(dev):
 
 
 @pytest.mark.parametrize("env", [{"MIORI_LMH_NWV": "12"}, {"MIORI_LMH_NWV": "16"},
-                                 {"MIORI_SKINNY_XROT": "1"}])
+                                 {"MIORI_SKINNY_XROT": "1"}, {"MIORI_LMH_XSUM": "1"}])
 def test_tuning_switch_is_bit_identical(dev, tmp_path, env):
     say(f"tuning switch {env} (child process)")
     ref = run_cases(dev)
